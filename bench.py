@@ -1,0 +1,258 @@
+"""Benchmark of Inkling relative-bias flash attention on one MI355X.
+
+Headline (the `value`): causal prefill over a batch of 8 sequences of 4096
+tokens, Hq 8 / Hkv 2, head_dim 128, bf16, per-head bias table [8,128]
+(rel_extent 128), one call of the prefill kernel per step.  Reported as
+TFLOP/s of algorithmic work, FLOPs = 4 * head_dim * (visible query-key pairs),
+with the reference's own 2*S^2*D*Hq*B count alongside.
+
+Also measured in the same run: split-KV decode (batch 64, one query per
+sequence, KV lengths U[1024,16384] seeded, non-causal so the whole cache is
+streamed) as KV GB/s against the 8 TB/s HBM peak; the other prefill sequence
+lengths {1024, 2048, 8192}; and the fp32 CPU oracle on a bounded sample as the
+CPU baseline.
+
+Usage:  python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
+        [--only prefill|decode|all] [--seq 4096]
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "inkling-fa4-relative-attention_amd"))
+sys.path.insert(0, REPO)
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _ensure_built():
+    pkg = os.path.join(REPO, "inkling-fa4-relative-attention_amd", "inkling_fa4")
+    if not (os.path.exists(os.path.join(pkg, "libifa4.so")) and
+            os.path.exists(os.path.join(pkg, "_ifa4_torch.so"))):
+        import __graft_entry__
+
+        __graft_entry__.build()
+
+
+def time_gpu(fn, steps, warmup):
+    """Average ms per call of `fn` over `steps` back-to-back calls, bracketed by
+    HIP events on the current stream (where the operator launches)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def time_gpu_samples(fn, steps, warmup):
+    """Per-call event timings (ms) for percentiles."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sorted(a.elapsed_time(b) for a, b in evs)
+
+
+def prefill_bench(seq_len, steps, warmup, batch=8):
+    import torch
+    from inkling_fa4 import inkling_fa4_rel_attention, testing
+
+    case = testing.long_prefill(seq_len, batch=batch)
+    pairs = case.visible_pairs()
+    d = case.q.shape[2]
+    hq = case.q.shape[1]
+    flops = 4.0 * d * pairs
+    flops_ref_formula = 2.0 * seq_len * seq_len * d * hq * batch
+    c = case.to("cuda")
+    args = c.args()
+
+    def step():
+        return inkling_fa4_rel_attention(*args, causal=True, softmax_scale=c.scale)
+
+    ms = time_gpu(step, steps, warmup)
+    samples = time_gpu_samples(step, max(10, min(steps, 50)), 2)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {
+        "seq_len": seq_len, "batch": batch, "ms": ms, "tflops": tflops,
+        "tflops_ref_formula": flops_ref_formula / (ms * 1e-3) / 1e12,
+        "flops": flops, "flops_ref_formula": flops_ref_formula,
+        "p10_ms": samples[len(samples) // 10], "p50_ms": samples[len(samples) // 2],
+        "p90_ms": samples[(9 * len(samples)) // 10],
+        "frac_of_peak": tflops / MFMA_BF16_PEAK_TFLOPS,
+    }, case
+
+
+def decode_bench(steps, warmup):
+    import torch
+    from inkling_fa4 import inkling_fa4_rel_attention_decode, testing
+
+    case = testing.decode(causal=False)
+    lens_k = (case.cu_k[1:] - case.cu_k[:-1])
+    sum_l = int(lens_k.sum())
+    hkv, d = case.k.shape[1], case.k.shape[2]
+    esize = case.k.element_size()
+    kv_bytes = sum_l * hkv * d * 2 * esize
+    qo_bytes = 2 * case.q.numel() * esize
+    c = case.to("cuda")
+    args = c.args()
+
+    def step():
+        return inkling_fa4_rel_attention_decode(*args, causal=False, softmax_scale=c.scale)
+
+    ms = time_gpu(step, steps, warmup)
+    gbps = (kv_bytes + qo_bytes) / (ms * 1e-3) / 1e9
+    return {"batch": case.q.shape[0], "sum_kv_len": sum_l, "bytes": kv_bytes + qo_bytes,
+            "us": ms * 1e3, "gbps": gbps, "frac_of_peak": gbps / HBM_PEAK_GBPS}
+
+
+def copy_bandwidth():
+    """Device-to-device copy bandwidth (GB/s, read + write) of a 1 GiB buffer."""
+    import torch
+
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    ms = time_gpu(lambda: b.copy_(a), 10, 3)
+    return 2 * n / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(case):
+    """fp32 CPU oracle on one sequence of the headline batch (all heads)."""
+    import torch
+    from oracle import ref_rel_attn
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    cq, ck = case.cu_q.tolist(), case.cu_k.tolist()
+    q = case.q[cq[0]:cq[1]]
+    k = case.k[ck[0]:ck[1]]
+    v = case.v[ck[0]:ck[1]]
+    rel = case.rel[cq[0]:cq[1]]
+    lq = cq[1] - cq[0]
+    cu = torch.tensor([0, lq], dtype=torch.int32)
+    pairs = lq * (lq + 1) // 2 * q.shape[1]
+    flops = 4.0 * q.shape[2] * pairs
+    t0 = time.perf_counter()
+    ref_rel_attn(q, k, v, rel, cu, cu, case.scale, case.rel_extent, causal=True)
+    dt = time.perf_counter() - t0
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port", "seconds": dt,
+            "sample": f"sequence 0 of the batch ({lq} tokens, all {q.shape[1]} heads), "
+                      f"fp32 oracle on the host CPU, os.cpu_count()={threads}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
+    ap.add_argument("--seq", type=int, default=4096)
+    ap.add_argument("--no-sweep", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    _ensure_built()
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev_name = torch.cuda.get_device_name(0)
+    log(f"device {dev_name}")
+
+    result = {
+        "metric": "prefill ms + TFLOPS @seq4096 Hq8/Hkv2 d128; decode KV GB/s; % roofline",
+        "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, N(0,0.5) bias table)",
+        "config": {"workload": f"causal prefill, batch 8 x seq {args.seq}, Hq 8, Hkv 2, "
+                               "head_dim 128, rel_extent 128, bf16",
+                   "global_batch": 8, "seq_len": args.seq, "parallelism": "single GPU"},
+    }
+    case = None
+    if args.only in ("all", "prefill"):
+        log(f"prefill seq {args.seq}: {args.steps} steps")
+        pre, case = prefill_bench(args.seq, args.steps, args.warmup)
+        log(f"prefill seq {args.seq}: {pre['ms']:.4f} ms  {pre['tflops']:.1f} TFLOP/s")
+        result["value"] = round(pre["tflops"], 2)
+        result["ms_per_step"] = round(pre["ms"], 5)
+        result["prefill"] = pre
+        result["roofline"] = {"bound": "mfma", "kernel": "prefill_fwd_kernel<128,bf16>",
+                              "achieved": round(pre["tflops"], 2),
+                              "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                              "frac": round(pre["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+                              "traffic": None}
+        if not args.no_sweep:
+            sweep = {}
+            for s in (1024, 2048, 8192):
+                if s == args.seq:
+                    continue
+                st = max(5, args.steps // (4 if s == 8192 else 1))
+                r, _ = prefill_bench(s, st, max(2, args.warmup // 2))
+                log(f"prefill seq {s}: {r['ms']:.4f} ms  {r['tflops']:.1f} TFLOP/s")
+                sweep[str(s)] = {"ms": round(r["ms"], 5), "tflops": round(r["tflops"], 2),
+                                 "frac_of_peak": round(r["frac_of_peak"], 4)}
+            result["prefill_sweep"] = sweep
+    if args.only in ("all", "decode"):
+        log(f"decode: {args.steps} steps")
+        dec = decode_bench(args.steps, args.warmup)
+        log(f"decode: {dec['us']:.1f} us  {dec['gbps']:.0f} GB/s")
+        result["decode"] = {**dec, "roofline": {"bound": "hbm", "kernel": "decode_split_kernel",
+                                                "achieved": round(dec["gbps"], 1),
+                                                "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                                                "frac": round(dec["frac_of_peak"], 4),
+                                                "traffic": None}}
+        if result["value"] is None:
+            result["value"] = round(dec["gbps"], 1)
+            result["unit"] = "GB/s"
+            result["ms_per_step"] = round(dec["us"] / 1e3, 5)
+            result["roofline"] = result["decode"]["roofline"]
+    try:
+        result["copy_gbps"] = round(copy_bandwidth(), 1)
+        log(f"device copy bandwidth: {result['copy_gbps']} GB/s")
+    except RuntimeError as e:  # out of memory on a busy device: report, continue
+        result["copy_gbps"] = None
+        log(f"copy bandwidth skipped: {e}")
+    if not args.skip_cpu and case is not None:
+        log("cpu baseline (fp32 oracle, one sequence)")
+        result["cpu_baseline"] = cpu_baseline(case)
+        log(f"cpu baseline: {result['cpu_baseline']['value']:.4f} TFLOP/s "
+            f"in {result['cpu_baseline']['seconds']:.1f} s")
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

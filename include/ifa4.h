@@ -1,0 +1,155 @@
+/*
+ * ifa4.h -- C ABI of the MI355X (gfx950) relative-bias flash attention library.
+ *
+ * The library (libifa4.so) holds hand-written HIP kernels for the forward pass
+ * of Inkling relative-position-bias attention.  It has no torch dependency: every
+ * argument is a plain pointer, size, stride or enum.  The caller owns every
+ * buffer; the library never allocates, frees or synchronises, and launches only
+ * on the stream it is given.  All entry points are re-entrant (the tile table is
+ * const) and return an ifa4_status; nothing throws or aborts across the ABI.
+ *
+ * Semantics are those of the reference oracle `ref_rel_attn`
+ * (src/inkling_fa4/reference.py:19-40):
+ *   for sequence b, local query i in [0,Lq), local key j in [0,Lk),
+ *   kv head kh = h / (n_heads / kv_heads),
+ *     s    = softmax_scale * <q[qs+i,h], k[ks+j,kh]>
+ *     dist = i + (Lq - Lk) - j;  s += rel[qs+i, h, dist]  iff 0 <= dist < rel_extent
+ *     visible iff (!causal || i >= j) && (window_left < 0 || i - j <= window_left)
+ *     out[qs+i,h] = softmax_j(s) @ v[ks+j,kh]           (written in the q dtype)
+ *     lse[h, qs+i] = ln sum_j exp(s)  over visible j     (fp32, optional)
+ * A row with no visible key gets out = 0 and lse = -inf (the reference oracle
+ * yields NaN there; the reference Triton kernels yield 0).
+ */
+#ifndef IFA4_H_
+#define IFA4_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IFA4_ABI_VERSION 1
+
+typedef enum ifa4_status {
+  IFA4_OK = 0,
+  IFA4_EINVAL = 1,        /* malformed argument: null pointer, bad size or stride */
+  IFA4_EUNSUPPORTED = 2,  /* well-formed but not implemented (head_dim, dtype mix) */
+  IFA4_EWORKSPACE = 3,    /* decode workspace missing or too small */
+  IFA4_ELAUNCH = 4        /* the HIP runtime reported an error at launch */
+} ifa4_status;
+
+typedef enum ifa4_dtype {
+  IFA4_BF16 = 0,
+  IFA4_FP16 = 1,
+  IFA4_FP32 = 2
+} ifa4_dtype;
+
+/* Debug flags (ifa4_args.flags). */
+#define IFA4_FLAG_NO_PRUNE 0x1u  /* visit every KV tile (pruning-invariance tests) */
+
+/*
+ * Arguments of one forward call.  Layouts (element strides, last dim contiguous):
+ *   q   [total_q, n_heads,  head_dim]   qkv_dtype
+ *   k,v [total_k, kv_heads, head_dim]   qkv_dtype
+ *   rel [total_q, n_heads,  rel_width]  rel_dtype, rel_width >= rel_extent;
+ *        rel_stride_t may be 0 (one per-head table shared by every token)
+ *   out [total_q, n_heads,  head_dim]   qkv_dtype
+ *   lse [n_heads, total_q] fp32 with head stride lse_stride_h (may be NULL)
+ *   cu_seqlens_q/k: device int32 [batch+1], non-decreasing, cu[0] = 0,
+ *        cu_q[batch] <= total_q, cu_k[batch] <= total_k.  Read only on the device.
+ * max_seqlen_q/k must bound every sequence length; they size the grid.
+ * Mirrors the argument list of inkling_fa4_rel_attention_triton
+ * (src/inkling_fa4/triton_kernel.py:85-89,99-105) plus softmax_scale and lse.
+ */
+typedef struct ifa4_args {
+  uint32_t struct_size;   /* sizeof(ifa4_args), checked by ifa4_validate */
+  uint32_t flags;         /* IFA4_FLAG_* */
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* rel;
+  void* out;
+  float* lse;
+  const int32_t* cu_seqlens_q;
+  const int32_t* cu_seqlens_k;
+  int64_t q_stride_t, q_stride_h;
+  int64_t k_stride_t, k_stride_h;
+  int64_t v_stride_t, v_stride_h;
+  int64_t rel_stride_t, rel_stride_h;
+  int64_t out_stride_t, out_stride_h;
+  int64_t lse_stride_h;
+  int64_t total_q, total_k;
+  int32_t batch;
+  int32_t n_heads;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t rel_extent;
+  int32_t rel_width;
+  int32_t max_seqlen_q;
+  int32_t max_seqlen_k;
+  int32_t window_left;    /* -1: no window */
+  int32_t causal;         /* 0 or 1; top-left aligned on local indices */
+  float softmax_scale;    /* > 0 */
+  int32_t qkv_dtype;      /* ifa4_dtype: IFA4_BF16 or IFA4_FP16 */
+  int32_t rel_dtype;      /* ifa4_dtype */
+} ifa4_args;
+
+/* Tile shape chosen for a call (the gfx950 tile table). */
+typedef struct ifa4_tile {
+  int32_t block_q;        /* query rows per workgroup */
+  int32_t block_k;        /* keys per KV tile */
+  int32_t waves;          /* wavefronts per workgroup */
+  int32_t stages;         /* LDS buffers for K/V */
+  int32_t kv_chunk;       /* decode: keys per split (0 for prefill) */
+} ifa4_tile;
+
+/* Human-readable name of a status code; never NULL. */
+const char* ifa4_status_str(int32_t status);
+
+/* ABI version the library was built with (IFA4_ABI_VERSION). */
+int32_t ifa4_abi_version(void);
+
+/* Pure host-side argument check; touches no device memory. */
+int32_t ifa4_validate(const ifa4_args* args);
+
+/*
+ * Prefill / varlen / chunked / sliding-window forward, one launch over every
+ * (query tile, head, sequence).  Replaces the per-sequence launch loop of
+ * inkling_fa4_rel_attention_triton (src/inkling_fa4/triton_kernel.py:84-107)
+ * and inkling_fa4_rel_attention_kv_pruned_triton
+ * (src/inkling_fa4/triton_kernel_kv_pruned.py:210-279).  stream: hipStream_t
+ * (NULL = the null stream).
+ */
+int32_t ifa4_prefill_fwd(const ifa4_args* args, void* stream);
+
+/* Tile shape ifa4_prefill_fwd uses for these arguments. */
+int32_t ifa4_prefill_tile(const ifa4_args* args, ifa4_tile* tile);
+
+/*
+ * Host-side count of the KV tiles the prefill kernel visits, using the same
+ * pruning rule as the device code, from host copies of cu_seqlens.  total =
+ * tiles an unpruned kernel would visit.  For reports and tests.
+ */
+int32_t ifa4_prefill_count_tiles(const ifa4_args* args, const int32_t* host_cu_seqlens_q,
+                                 const int32_t* host_cu_seqlens_k, int64_t* visited,
+                                 int64_t* total);
+
+/*
+ * Decode: exactly one query token per sequence (total_q == batch).  Split-KV:
+ * pass 1 writes one (o, lse) partial per (sequence, head, KV split) into the
+ * workspace, pass 2 merges the splits by log-sum-exp and writes out/lse.
+ * Replaces inkling_fa4_rel_attention_decode_triton
+ * (src/inkling_fa4/triton_kernel_decode.py:127-170).
+ */
+size_t ifa4_decode_workspace_bytes(const ifa4_args* args);
+int32_t ifa4_decode_tile(const ifa4_args* args, ifa4_tile* tile);
+int32_t ifa4_decode_fwd(const ifa4_args* args, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* IFA4_H_ */

@@ -1,0 +1,265 @@
+// C ABI of the gfx950 relative-bias attention library: argument validation,
+// tile selection and kernel dispatch.  Declared in include/ifa4.h.
+//
+// The reference has no validation at all (src/inkling_fa4/triton_kernel.py:84-107:
+// bad shapes surface as Triton errors or silent out-of-bounds reads); here every
+// entry point checks its arguments on the host before anything is launched and
+// reports a status code.
+#include "ifa4.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "ifa4_kernels.h"
+#include "tile_table.h"
+
+namespace {
+
+constexpr float kLog2eHost = 1.4426950408889634f;
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int32_t check_args(const ifa4_args* a) {
+  if (a == nullptr) return IFA4_EINVAL;
+  if (a->struct_size != sizeof(ifa4_args)) return IFA4_EINVAL;
+  if (a->batch < 0 || a->n_heads < 1 || a->kv_heads < 1) return IFA4_EINVAL;
+  if (a->n_heads % a->kv_heads != 0) return IFA4_EINVAL;
+  if (a->total_q < 0 || a->total_k < 0) return IFA4_EINVAL;
+  if (a->max_seqlen_q < 0 || a->max_seqlen_k < 0) return IFA4_EINVAL;
+  if (a->rel_extent < 0 || a->rel_width < a->rel_extent) return IFA4_EINVAL;
+  if (a->window_left < -1) return IFA4_EINVAL;
+  if (a->causal != 0 && a->causal != 1) return IFA4_EINVAL;
+  if (a->qkv_dtype < IFA4_BF16 || a->qkv_dtype > IFA4_FP32) return IFA4_EINVAL;
+  if (a->rel_dtype < IFA4_BF16 || a->rel_dtype > IFA4_FP32) return IFA4_EINVAL;
+  if (a->head_dim < 1) return IFA4_EINVAL;
+  if (a->q_stride_t < 0 || a->q_stride_h < 0 || a->k_stride_t < 0 || a->k_stride_h < 0 ||
+      a->v_stride_t < 0 || a->v_stride_h < 0 || a->rel_stride_t < 0 || a->rel_stride_h < 0 ||
+      a->out_stride_t < 0 || a->out_stride_h < 0 || a->lse_stride_h < 0)
+    return IFA4_EINVAL;
+  if (!(std::isfinite(a->softmax_scale))) return IFA4_EINVAL;
+  if (a->batch == 0) return IFA4_OK;  // nothing to read or write
+  if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->out == nullptr ||
+      a->cu_seqlens_q == nullptr || a->cu_seqlens_k == nullptr)
+    return IFA4_EINVAL;
+  if (a->rel_extent > 0 && a->rel == nullptr) return IFA4_EINVAL;
+  if (a->lse != nullptr) {
+    if (!aligned(a->lse, 4)) return IFA4_EINVAL;
+    if (a->n_heads > 1 && a->lse_stride_h < a->total_q) return IFA4_EINVAL;
+  }
+  // Supported, not just well-formed.
+  if (a->head_dim != 64 && a->head_dim != 128) return IFA4_EUNSUPPORTED;
+  if (a->qkv_dtype == IFA4_FP32) return IFA4_EUNSUPPORTED;
+  if (!(a->softmax_scale > 0.f)) return IFA4_EUNSUPPORTED;
+  // 16-byte vector loads of q/k/v rows, 8-byte stores of out rows.
+  if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->out, 16))
+    return IFA4_EUNSUPPORTED;
+  if ((a->q_stride_t | a->q_stride_h | a->k_stride_t | a->k_stride_h | a->v_stride_t |
+       a->v_stride_h | a->out_stride_t | a->out_stride_h) % 8 != 0)
+    return IFA4_EUNSUPPORTED;
+  if (a->rel != nullptr && !aligned(a->rel, a->rel_dtype == IFA4_FP32 ? 4 : 2))
+    return IFA4_EINVAL;
+  return IFA4_OK;
+}
+
+ifa4::PrefillParams make_prefill_params(const ifa4_args* a) {
+  ifa4::PrefillParams p{};
+  p.q = a->q;
+  p.k = a->k;
+  p.v = a->v;
+  p.rel = a->rel;
+  p.out = a->out;
+  p.lse = a->lse;
+  p.cu_q = a->cu_seqlens_q;
+  p.cu_k = a->cu_seqlens_k;
+  p.q_st = a->q_stride_t;
+  p.q_sh = a->q_stride_h;
+  p.k_st = a->k_stride_t;
+  p.k_sh = a->k_stride_h;
+  p.v_st = a->v_stride_t;
+  p.v_sh = a->v_stride_h;
+  p.rel_st = a->rel_stride_t;
+  p.rel_sh = a->rel_stride_h;
+  p.o_st = a->out_stride_t;
+  p.o_sh = a->out_stride_h;
+  p.lse_sh = a->lse_stride_h;
+  p.batch = a->batch;
+  p.n_heads = a->n_heads;
+  p.group = a->n_heads / a->kv_heads;
+  p.rel_extent = a->rel_extent;
+  p.window_left = a->window_left;
+  p.causal = a->causal;
+  p.no_prune = (a->flags & IFA4_FLAG_NO_PRUNE) ? 1 : 0;
+  p.rel_dtype = a->rel_dtype;
+  const int bq = ifa4::prefill_block_q();
+  p.n_qtiles = (a->max_seqlen_q + bq - 1) / bq;
+  p.scale_log2 = a->softmax_scale * kLog2eHost;
+  return p;
+}
+
+int64_t decode_splits(const ifa4_args* a, int32_t chunk) {
+  const int64_t keys = a->causal ? (a->max_seqlen_k > 0 ? 1 : 0) : a->max_seqlen_k;
+  const int64_t s = (keys + chunk - 1) / chunk;
+  return s < 1 ? 1 : s;
+}
+
+int32_t decode_chunk(const ifa4_args* a) {
+  return ifa4::decode_chunk_for(a->batch, a->kv_heads, a->max_seqlen_k);
+}
+
+int32_t check_decode(const ifa4_args* a) {
+  const int32_t st = check_args(a);
+  if (st != IFA4_OK) return st;
+  if (a->batch > 0 && a->total_q != a->batch) return IFA4_EINVAL;  // one query per sequence
+  if (a->n_heads / a->kv_heads > ifa4::decode_max_group()) return IFA4_EUNSUPPORTED;
+  return IFA4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ifa4_status_str(int32_t status) {
+  switch (status) {
+    case IFA4_OK: return "IFA4_OK";
+    case IFA4_EINVAL: return "IFA4_EINVAL: invalid argument";
+    case IFA4_EUNSUPPORTED: return "IFA4_EUNSUPPORTED: argument combination not supported";
+    case IFA4_EWORKSPACE: return "IFA4_EWORKSPACE: workspace missing or too small";
+    case IFA4_ELAUNCH: return "IFA4_ELAUNCH: kernel launch failed";
+    default: return "IFA4: unknown status";
+  }
+}
+
+int32_t ifa4_abi_version(void) { return IFA4_ABI_VERSION; }
+
+int32_t ifa4_validate(const ifa4_args* args) { return check_args(args); }
+
+int32_t ifa4_prefill_tile(const ifa4_args* args, ifa4_tile* tile) {
+  if (args == nullptr || tile == nullptr) return IFA4_EINVAL;
+  for (const auto& e : ifa4::kPrefillTiles) {
+    if (e.head_dim == args->head_dim) {
+      tile->block_q = e.block_q;
+      tile->block_k = e.block_k;
+      tile->waves = e.waves;
+      tile->stages = e.stages;
+      tile->kv_chunk = 0;
+      return IFA4_OK;
+    }
+  }
+  return IFA4_EUNSUPPORTED;
+}
+
+int32_t ifa4_prefill_fwd(const ifa4_args* args, void* stream) {
+  const int32_t st = check_args(args);
+  if (st != IFA4_OK) return st;
+  if (args->batch == 0 || args->max_seqlen_q == 0) return IFA4_OK;
+  const ifa4::PrefillParams p = make_prefill_params(args);
+  const hipError_t e = ifa4::launch_prefill(p, args->head_dim, args->qkv_dtype,
+                                            static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IFA4_OK : IFA4_ELAUNCH;
+}
+
+int32_t ifa4_prefill_count_tiles(const ifa4_args* args, const int32_t* cu_q, const int32_t* cu_k,
+                                 int64_t* visited, int64_t* total) {
+  if (args == nullptr || cu_q == nullptr || cu_k == nullptr || visited == nullptr ||
+      total == nullptr)
+    return IFA4_EINVAL;
+  if (args->batch < 0 || args->n_heads < 1) return IFA4_EINVAL;
+  const int bq = ifa4::prefill_block_q();
+  const int bk = ifa4::prefill_block_k();
+  const bool no_prune = (args->flags & IFA4_FLAG_NO_PRUNE) != 0;
+  int64_t vis = 0, tot = 0;
+  for (int b = 0; b < args->batch; ++b) {
+    const int lq = cu_q[b + 1] - cu_q[b];
+    const int lk = cu_k[b + 1] - cu_k[b];
+    if (lq < 0 || lk < 0) return IFA4_EINVAL;
+    for (int q0 = 0; q0 < lq; q0 += bq) {
+      const int q_hi = q0 + bq < lq ? q0 + bq : lq;
+      int kend = lk, kbeg = 0;
+      if (!no_prune) {
+        if (args->causal) kend = kend < q_hi ? kend : q_hi;
+        if (args->window_left >= 0) kbeg = q0 - args->window_left > 0 ? q0 - args->window_left : 0;
+      }
+      const int kt_beg = kbeg / bk;
+      const int kt_end = kend > kbeg ? (kend + bk - 1) / bk : kt_beg;
+      vis += (int64_t)(kt_end - kt_beg) * args->n_heads;
+      tot += (int64_t)((lk + bk - 1) / bk) * args->n_heads;
+    }
+  }
+  *visited = vis;
+  *total = tot;
+  return IFA4_OK;
+}
+
+size_t ifa4_decode_workspace_bytes(const ifa4_args* args) {
+  if (check_decode(args) != IFA4_OK) return 0;
+  const int64_t splits = decode_splits(args, decode_chunk(args));
+  const int64_t rows = (int64_t)args->batch * args->n_heads * splits;
+  const int64_t o_bytes = ((rows * args->head_dim * 4) + 255) / 256 * 256;
+  return (size_t)(o_bytes + rows * 4);
+}
+
+int32_t ifa4_decode_tile(const ifa4_args* args, ifa4_tile* tile) {
+  if (tile == nullptr) return IFA4_EINVAL;
+  const int32_t st = check_decode(args);
+  if (st != IFA4_OK) return st;
+  tile->block_q = 1;
+  tile->block_k = 64;
+  tile->waves = 1;
+  tile->stages = 1;
+  tile->kv_chunk = decode_chunk(args);
+  return IFA4_OK;
+}
+
+int32_t ifa4_decode_fwd(const ifa4_args* args, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  const int32_t st = check_decode(args);
+  if (st != IFA4_OK) return st;
+  if (args->batch == 0) return IFA4_OK;
+  const size_t need = ifa4_decode_workspace_bytes(args);
+  if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256))
+    return IFA4_EWORKSPACE;
+  const int32_t chunk = decode_chunk(args);
+  const int64_t splits = decode_splits(args, chunk);
+  const int64_t rows = (int64_t)args->batch * args->n_heads * splits;
+  const int64_t o_bytes = ((rows * args->head_dim * 4) + 255) / 256 * 256;
+
+  ifa4::DecodeParams p{};
+  p.q = args->q;
+  p.k = args->k;
+  p.v = args->v;
+  p.rel = args->rel;
+  p.out = args->out;
+  p.lse = args->lse;
+  p.cu_q = args->cu_seqlens_q;
+  p.cu_k = args->cu_seqlens_k;
+  p.ws_o = static_cast<float*>(workspace);
+  p.ws_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes);
+  p.q_st = args->q_stride_t;
+  p.q_sh = args->q_stride_h;
+  p.k_st = args->k_stride_t;
+  p.k_sh = args->k_stride_h;
+  p.v_st = args->v_stride_t;
+  p.v_sh = args->v_stride_h;
+  p.rel_st = args->rel_stride_t;
+  p.rel_sh = args->rel_stride_h;
+  p.o_st = args->out_stride_t;
+  p.o_sh = args->out_stride_h;
+  p.lse_sh = args->lse_stride_h;
+  p.batch = args->batch;
+  p.n_heads = args->n_heads;
+  p.kv_heads = args->kv_heads;
+  p.group = args->n_heads / args->kv_heads;
+  p.rel_extent = args->rel_extent;
+  p.causal = args->causal;
+  p.rel_dtype = args->rel_dtype;
+  p.chunk = chunk;
+  p.n_splits = (int32_t)splits;
+  p.scale_log2 = args->softmax_scale * kLog2eHost;
+  const hipError_t e = ifa4::launch_decode(p, args->head_dim, args->qkv_dtype,
+                                           static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IFA4_OK : IFA4_ELAUNCH;
+}
+
+}  // extern "C"

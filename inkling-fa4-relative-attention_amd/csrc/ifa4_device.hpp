@@ -1,0 +1,109 @@
+// Device-side helpers shared by the gfx950 kernels: operand types, MFMA
+// wrappers, wave-level exchanges and element conversions.
+//
+// Wave64 MFMA layouts used throughout (CDNA3/CDNA4 "32x32" and "16x16" forms):
+//   v_mfma_f32_32x32x16_{bf16,f16}:  lane l, g = l / 32
+//     A (32 x 16):  row l % 32, eight k-slots 8g .. 8g+7
+//     B (16 x 32):  col l % 32, eight k-slots 8g .. 8g+7
+//     C (32 x 32):  acc[4*i + j] = C[8*i + 4*g + j][l % 32]   (i, j in 0..3)
+//   v_mfma_f32_16x16x32_{bf16,f16}:  lane l, g = l / 16
+//     A (16 x 32):  row l % 16, k-slots 8g .. 8g+7
+//     B (32 x 16):  col l % 16, k-slots 8g .. 8g+7
+//     C (16 x 16):  acc[j] = C[4*g + j][l % 16]
+// A k-slot of A is multiplied with the same k-slot of B, so which physical
+// index a slot stands for is a free choice as long as A and B agree.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ifa4 {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// Deferred-rescale threshold (log2 units): the running max used for the
+// exponentials is only raised when a row's max grows by more than this, so
+// p <= 2^8 stays exact in fp32 and representable in bf16/fp16.
+constexpr float kRescaleThreshold = 8.0f;
+
+struct Bf16Tag {};
+struct F16Tag {};
+
+template <typename Tag> struct Elem;
+template <> struct Elem<Bf16Tag> {
+  // Two fp32 -> packed 16-bit pair (round to nearest even).
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  static __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+template <> struct Elem<F16Tag> {
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    f16x2_t v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  static __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+// Bias element of dtype code `rel_dtype` (0 bf16, 1 fp16, 2 fp32) as fp32.
+__device__ __forceinline__ float load_rel(const void* base, int64_t idx, int rel_dtype) {
+  if (rel_dtype == 2) return static_cast<const float*>(base)[idx];
+  uint32_t bits = static_cast<const uint16_t*>(base)[idx];
+  if (rel_dtype == 0) return __uint_as_float(bits << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// max(x[lane], x[lane ^ 32]) in every lane.
+__device__ __forceinline__ float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// x[lane] + x[lane ^ 32] in every lane.
+__device__ __forceinline__ float add_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ bool wave_any(bool p) {
+  return __builtin_amdgcn_ballot_w64(p) != 0;
+}
+
+__device__ __forceinline__ u32x4_t ld_global_16(const void* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+
+}  // namespace ifa4

@@ -1,0 +1,64 @@
+// Internal interface between the C ABI layer (ifa4_api.cpp) and the HIP
+// kernels.  Not installed; the public interface is include/ifa4.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ifa4 {
+
+struct PrefillParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* rel;
+  void* out;
+  float* lse;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, rel_st, rel_sh, o_st, o_sh, lse_sh;
+  int32_t batch;
+  int32_t n_heads;
+  int32_t group;        // n_heads / kv_heads
+  int32_t rel_extent;
+  int32_t window_left;  // -1: none
+  int32_t causal;
+  int32_t no_prune;
+  int32_t rel_dtype;    // 0 bf16, 1 fp16, 2 fp32
+  int32_t n_qtiles;     // ceil(max_seqlen_q / block_q)
+  float scale_log2;     // softmax_scale * log2(e)
+};
+
+struct DecodeParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* rel;
+  void* out;
+  float* lse;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  float* ws_o;    // [batch, n_heads, n_splits, head_dim]
+  float* ws_lse;  // [batch, n_heads, n_splits] (log2 domain)
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, rel_st, rel_sh, o_st, o_sh, lse_sh;
+  int32_t batch;
+  int32_t n_heads;
+  int32_t kv_heads;
+  int32_t group;
+  int32_t rel_extent;
+  int32_t causal;
+  int32_t rel_dtype;
+  int32_t chunk;     // keys per split (multiple of 64)
+  int32_t n_splits;  // ceil(max_seqlen_k / chunk)
+  float scale_log2;
+};
+
+int prefill_block_q();
+int prefill_block_k();
+int prefill_waves();
+hipError_t launch_prefill(const PrefillParams& p, int head_dim, int qkv_dtype, hipStream_t stream);
+
+int decode_max_group();
+hipError_t launch_decode(const DecodeParams& p, int head_dim, int qkv_dtype, hipStream_t stream);
+
+}  // namespace ifa4

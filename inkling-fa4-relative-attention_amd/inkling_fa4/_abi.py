@@ -1,0 +1,134 @@
+"""ctypes view of the C ABI in include/ifa4.h (libifa4.so).
+
+Used for host-only queries (tile table, tile counts, argument validation) and
+by tests that call the library directly.  The compute path goes through the
+torch binding (`_native.py`), which calls the same library.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libifa4.so")
+
+IFA4_OK = 0
+IFA4_EINVAL = 1
+IFA4_EUNSUPPORTED = 2
+IFA4_EWORKSPACE = 3
+IFA4_ELAUNCH = 4
+
+IFA4_BF16 = 0
+IFA4_FP16 = 1
+IFA4_FP32 = 2
+
+IFA4_FLAG_NO_PRUNE = 0x1
+
+# Every function include/ifa4.h declares: name -> (restype, argtypes).
+_c_int32 = ctypes.c_int32
+_c_int64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+
+
+class Ifa4Args(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
+        ("q", _vp), ("k", _vp), ("v", _vp), ("rel", _vp),
+        ("out", _vp), ("lse", _vp),
+        ("cu_seqlens_q", _vp), ("cu_seqlens_k", _vp),
+        ("q_stride_t", _c_int64), ("q_stride_h", _c_int64),
+        ("k_stride_t", _c_int64), ("k_stride_h", _c_int64),
+        ("v_stride_t", _c_int64), ("v_stride_h", _c_int64),
+        ("rel_stride_t", _c_int64), ("rel_stride_h", _c_int64),
+        ("out_stride_t", _c_int64), ("out_stride_h", _c_int64),
+        ("lse_stride_h", _c_int64),
+        ("total_q", _c_int64), ("total_k", _c_int64),
+        ("batch", _c_int32), ("n_heads", _c_int32), ("kv_heads", _c_int32),
+        ("head_dim", _c_int32), ("rel_extent", _c_int32), ("rel_width", _c_int32),
+        ("max_seqlen_q", _c_int32), ("max_seqlen_k", _c_int32),
+        ("window_left", _c_int32), ("causal", _c_int32),
+        ("softmax_scale", ctypes.c_float),
+        ("qkv_dtype", _c_int32), ("rel_dtype", _c_int32),
+    ]
+
+
+class Ifa4Tile(ctypes.Structure):
+    _fields_ = [("block_q", _c_int32), ("block_k", _c_int32), ("waves", _c_int32),
+                ("stages", _c_int32), ("kv_chunk", _c_int32)]
+
+
+_P_ARGS = ctypes.POINTER(Ifa4Args)
+_P_TILE = ctypes.POINTER(Ifa4Tile)
+_P_I32 = ctypes.POINTER(ctypes.c_int32)
+_P_I64 = ctypes.POINTER(ctypes.c_int64)
+
+SIGNATURES = {
+    "ifa4_status_str": (ctypes.c_char_p, [_c_int32]),
+    "ifa4_abi_version": (_c_int32, []),
+    "ifa4_validate": (_c_int32, [_P_ARGS]),
+    "ifa4_prefill_fwd": (_c_int32, [_P_ARGS, _vp]),
+    "ifa4_prefill_tile": (_c_int32, [_P_ARGS, _P_TILE]),
+    "ifa4_prefill_count_tiles": (_c_int32, [_P_ARGS, _P_I32, _P_I32, _P_I64, _P_I64]),
+    "ifa4_decode_workspace_bytes": (ctypes.c_size_t, [_P_ARGS]),
+    "ifa4_decode_tile": (_c_int32, [_P_ARGS, _P_TILE]),
+    "ifa4_decode_fwd": (_c_int32, [_P_ARGS, _vp, ctypes.c_size_t, _vp]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libifa4.so once; raise ImportError with the build hint if absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing; build it with "
+                "`python inkling-fa4-relative-attention_amd/build.py`")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, argt) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = argt
+        _lib = handle
+    return _lib
+
+
+def status_str(code):
+    return lib().ifa4_status_str(code).decode()
+
+
+def make_args(**kw):
+    """Ifa4Args with struct_size filled and sane defaults, overridden by kw."""
+    a = Ifa4Args()
+    a.struct_size = ctypes.sizeof(Ifa4Args)
+    a.window_left = -1
+    a.causal = 1
+    a.softmax_scale = 1.0
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def prefill_tile(head_dim):
+    t = Ifa4Tile()
+    st = lib().ifa4_prefill_tile(ctypes.byref(make_args(head_dim=head_dim)), ctypes.byref(t))
+    if st != IFA4_OK:
+        raise ValueError(status_str(st))
+    return t
+
+
+def count_tiles(cu_q, cu_k, n_heads, block_args=None, causal=True, window_left=-1,
+                no_prune=False, head_dim=128):
+    """KV tiles the prefill kernel visits vs an unpruned kernel (host count)."""
+    batch = len(cu_q) - 1
+    a = make_args(batch=batch, n_heads=n_heads, kv_heads=1, head_dim=head_dim,
+                  causal=int(causal), window_left=window_left,
+                  flags=IFA4_FLAG_NO_PRUNE if no_prune else 0)
+    cq = (ctypes.c_int32 * len(cu_q))(*[int(x) for x in cu_q])
+    ck = (ctypes.c_int32 * len(cu_k))(*[int(x) for x in cu_k])
+    vis, tot = ctypes.c_int64(), ctypes.c_int64()
+    st = lib().ifa4_prefill_count_tiles(ctypes.byref(a), cq, ck, ctypes.byref(vis),
+                                        ctypes.byref(tot))
+    if st != IFA4_OK:
+        raise ValueError(status_str(st))
+    return vis.value, tot.value

@@ -1,0 +1,46 @@
+"""Tile presets, gfx950 edition.
+
+Same public surface as src/inkling_fa4/autotune_configs.py:17-85 (`PRESETS`,
+`_detect_arch`, `get_preset`) so callers that print or pass presets keep
+working.  On MI355X the tile shape is a property of the compiled HIP kernel;
+the values are read from the library's tile table (ifa4_prefill_tile), and
+`num_warps` counts 64-wide wavefronts.  The reference's sm86/sm90/sm100 rows
+are not carried over: they tune Triton kernels that do not exist here.
+"""
+import functools
+
+from . import _abi
+
+
+@functools.lru_cache(maxsize=None)
+def _gfx950_row(head_dim=128):
+    t = _abi.prefill_tile(head_dim)
+    return (t.block_q, t.block_k, t.waves, t.stages)
+
+
+def __getattr__(name):
+    # PRESETS is built on first access (it queries libifa4.so).
+    if name == "PRESETS":
+        bq, bk, w, st = _gfx950_row(128)
+        return {"gfx950": {"default": (bq, bk, w, st), "buckets": []}}
+    raise AttributeError(name)
+
+
+def _detect_arch() -> str:
+    """'gfx950' on MI355X; the GCN arch name of another AMD GPU; 'gfx950' when
+    no GPU is visible (the library is built for gfx950 only)."""
+    import torch
+
+    if not torch.cuda.is_available():
+        return "gfx950"
+    name = getattr(torch.cuda.get_device_properties(0), "gcnArchName", "gfx950")
+    return name.split(":")[0]
+
+
+def get_preset(seq_len: int, arch: str | None = None, head_dim: int = 128) -> dict:
+    """Tile config used for `seq_len` query tokens: BLOCK_Q, BLOCK_K,
+    num_warps (wavefronts) and num_stages (LDS buffers).  `arch` is accepted
+    for signature compatibility; every arch maps to the gfx950 table."""
+    del seq_len, arch
+    bq, bk, w, s = _gfx950_row(head_dim)
+    return {"BLOCK_Q": bq, "BLOCK_K": bk, "num_warps": w, "num_stages": s}

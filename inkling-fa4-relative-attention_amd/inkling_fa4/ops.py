@@ -1,0 +1,156 @@
+"""Python operator API of Inkling relative-bias flash attention on MI355X.
+
+Drop-in for the reference's Triton wrappers, same names and positional
+signatures:
+
+  inkling_fa4_rel_attention_triton            src/inkling_fa4/triton_kernel.py:84-107
+  inkling_fa4_rel_attention_kv_pruned_triton  src/inkling_fa4/triton_kernel_kv_pruned.py:210-279
+  inkling_fa4_rel_attention_decode_triton     src/inkling_fa4/triton_kernel_decode.py:127-170
+
+plus the same entry points under names without the `_triton` suffix.
+
+Differences from the reference wrappers (all deliberate):
+  * one kernel launch for the whole batch and no host synchronisation (the
+    reference reads every cu_seqlens entry to the host, triton_kernel.py:95);
+    `max_seqlen_q/k` must therefore bound every sequence length;
+  * keyword-only `softmax_scale` (default 1/head_dim, what the reference
+    prefill kernel hard-codes at triton_kernel.py:55) and `return_lse`
+    (returns (out, lse) with lse [n_heads, total_q] fp32, natural log);
+  * `head_dim`, `n_heads`, `kv_heads` default to the tensor shapes; an explicit
+    value that disagrees with the shapes raises (the reference reads out of
+    bounds, triton_kernel.py:33-37);
+  * `window_size[1]` is accepted and ignored, as in the reference
+    (triton_kernel.py:105 passes only window_size[0]);
+  * `arch` is accepted and ignored: gfx950 has one tile table;
+  * a row with no visible key yields out = 0 and lse = -inf;
+  * every input is validated; errors raise instead of reading out of bounds.
+The decode entry point uses the same default scale as prefill (1/head_dim);
+the reference decode kernel uses 1/sqrt(head_dim)
+(triton_kernel_decode.py:57), inconsistent with its prefill kernel.
+"""
+import math
+
+import torch
+
+from . import _abi
+from ._native import ops as _ops
+
+
+def _resolve(q, k, n_heads, kv_heads, head_dim, softmax_scale):
+    if q.dim() != 3 or k.dim() != 3:
+        raise ValueError("q and k must be [tokens, heads, head_dim]")
+    hq, d = q.shape[1], q.shape[2]
+    hkv = k.shape[1]
+    if n_heads is not None and n_heads != hq:
+        raise ValueError(f"n_heads={n_heads} disagrees with q.shape[1]={hq}")
+    if kv_heads is not None and kv_heads != hkv:
+        raise ValueError(f"kv_heads={kv_heads} disagrees with k.shape[1]={hkv}")
+    if head_dim is not None and head_dim != d:
+        raise ValueError(f"head_dim={head_dim} disagrees with q.shape[-1]={d}")
+    if hq % hkv:
+        raise ValueError(f"n_heads={hq} is not a multiple of kv_heads={hkv}")
+    scale = (1.0 / d) if softmax_scale is None else float(softmax_scale)
+    return scale
+
+
+def _window_left(window_size):
+    if window_size is None:
+        return -1
+    left = int(window_size[0])
+    return left if left >= 0 else -1
+
+
+@torch.no_grad()
+def inkling_fa4_rel_attention(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
+                              max_seqlen_q, max_seqlen_k, rel_extent, causal=True,
+                              window_size=(-1, -1), n_heads=None, kv_heads=None,
+                              head_dim=None, arch=None, *, softmax_scale=None,
+                              return_lse=False, _flags=0):
+    """Varlen / GQA / chunked / sliding-window prefill forward.
+
+    q [total_q, Hq, D], k/v [total_k, Hkv, D] (bf16 or fp16, last dim contiguous),
+    rel_logits [total_q, Hq, R' >= rel_extent] (bf16/fp16/fp32, any token stride
+    including 0), cu_seqlens_q/k int32 [batch+1] on the same GPU.
+    Returns out [total_q, Hq, D] in q.dtype, or (out, lse) with return_lse.
+    """
+    scale = _resolve(q, k, n_heads, kv_heads, head_dim, softmax_scale)
+    out, lse = _ops().fwd(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
+                          int(max_seqlen_k), int(rel_extent), bool(causal),
+                          _window_left(window_size), scale, bool(return_lse), int(_flags))
+    return (out, lse) if return_lse else out
+
+
+@torch.no_grad()
+def inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
+                                     max_seqlen_q, max_seqlen_k, rel_extent, causal=True,
+                                     window_size=(-1, -1), n_heads=None, kv_heads=None,
+                                     head_dim=None, arch=None, *, softmax_scale=None,
+                                     return_lse=False):
+    """Decode forward: exactly one query token per sequence
+    (cu_seqlens_q == arange(batch + 1)), KV split across workgroups and merged
+    by log-sum-exp.  Falls through to the prefill kernel when q holds more
+    tokens than there are sequences, or for GQA groups above 16."""
+    scale = _resolve(q, k, n_heads, kv_heads, head_dim, softmax_scale)
+    batch = cu_seqlens_q.shape[0] - 1
+    group = q.shape[1] // k.shape[1]
+    if q.shape[0] != batch or group > 16:
+        return inkling_fa4_rel_attention(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
+                                         max_seqlen_q, max_seqlen_k, rel_extent, causal,
+                                         window_size, softmax_scale=scale,
+                                         return_lse=return_lse)
+    out, lse = _ops().decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
+                             int(max_seqlen_q), int(max_seqlen_k), int(rel_extent), bool(causal),
+                             _window_left(window_size), scale, bool(return_lse), 0)
+    return (out, lse) if return_lse else out
+
+
+def inkling_fa4_rel_attention_triton(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
+                                     max_seqlen_q, max_seqlen_k, rel_extent, causal=True,
+                                     window_size=(-1, -1), n_heads=None, kv_heads=None,
+                                     head_dim=None, arch=None, **kw):
+    """Name kept from src/inkling_fa4/triton_kernel.py:85; runs the HIP kernel."""
+    return inkling_fa4_rel_attention(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
+                                     max_seqlen_q, max_seqlen_k, rel_extent, causal,
+                                     window_size, n_heads, kv_heads, head_dim, arch, **kw)
+
+
+def inkling_fa4_rel_attention_kv_pruned_triton(q, k, v, rel_logits, cu_seqlens_q,
+                                               cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                               rel_extent, causal=True, window_size=(-1, -1),
+                                               n_heads=None, kv_heads=None, head_dim=None,
+                                               arch=None, **kw):
+    """Name kept from src/inkling_fa4/triton_kernel_kv_pruned.py:210; the HIP
+    prefill kernel always prunes fully-masked KV tiles."""
+    return inkling_fa4_rel_attention(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
+                                     max_seqlen_q, max_seqlen_k, rel_extent, causal,
+                                     window_size, n_heads, kv_heads, head_dim, arch, **kw)
+
+
+def inkling_fa4_rel_attention_decode_triton(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
+                                            max_seqlen_q, max_seqlen_k, rel_extent, causal=True,
+                                            window_size=(-1, -1), n_heads=None, kv_heads=None,
+                                            head_dim=None, arch=None, **kw):
+    """Name kept from src/inkling_fa4/triton_kernel_decode.py:128."""
+    return inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
+                                            max_seqlen_q, max_seqlen_k, rel_extent, causal,
+                                            window_size, n_heads, kv_heads, head_dim, arch, **kw)
+
+
+def prefill_tile_counts(cu_seqlens_q, cu_seqlens_k, n_heads, causal=True, window_size=(-1, -1),
+                        head_dim=128):
+    """(visited, total) KV tiles of a prefill call: tiles the kernel loads after
+    causal/window pruning vs tiles an unpruned kernel would load."""
+    cq = [int(x) for x in torch.as_tensor(cu_seqlens_q).cpu().tolist()]
+    ck = [int(x) for x in torch.as_tensor(cu_seqlens_k).cpu().tolist()]
+    return _abi.count_tiles(cq, ck, n_heads, causal=causal,
+                            window_left=_window_left(window_size), head_dim=head_dim)
+
+
+def default_scale(head_dim):
+    """Default softmax scale of the drop-in API (1/head_dim)."""
+    return 1.0 / head_dim
+
+
+def sdpa_scale(head_dim):
+    """The conventional 1/sqrt(head_dim) scale."""
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,195 @@
+"""CPU tests of the C ABI: the library loads, exports every symbol the header
+declares, validates arguments on the host, and its tile pruning rule visits
+exactly the KV tiles that hold a visible (query, key) pair."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from inkling_fa4 import _abi, autotune_configs
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "ifa4.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ifa4_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    for must in ("ifa4_validate", "ifa4_prefill_fwd", "ifa4_decode_fwd",
+                 "ifa4_decode_workspace_bytes", "ifa4_status_str"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _abi.lib()
+    names = _declared_functions()
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_abi.SIGNATURES), "ctypes view out of sync with include/ifa4.h"
+    nm = subprocess.run(["nm", "-D", "--defined-only", _abi.LIB_PATH], capture_output=True,
+                        text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s(ifa4_\w+)", nm))
+    assert set(names) <= exported
+
+
+def test_abi_version_and_struct_size():
+    assert _abi.lib().ifa4_abi_version() == 1
+    a = _abi.make_args()
+    a.struct_size = 12
+    assert _abi.lib().ifa4_validate(ctypes.byref(a)) == _abi.IFA4_EINVAL
+
+
+def test_status_strings():
+    for code in range(5):
+        assert _abi.status_str(code).startswith("IFA4")
+    assert "unknown" in _abi.status_str(99)
+
+
+# fake, well-aligned device addresses: ifa4_validate never dereferences them
+_P = 1 << 20
+
+
+def _good(**kw):
+    base = dict(batch=2, n_heads=8, kv_heads=2, head_dim=128, rel_extent=128, rel_width=128,
+                max_seqlen_q=64, max_seqlen_k=64, total_q=128, total_k=128,
+                q=_P, k=2 * _P, v=3 * _P, rel=4 * _P, out=5 * _P,
+                cu_seqlens_q=6 * _P, cu_seqlens_k=7 * _P,
+                q_stride_t=8 * 128, q_stride_h=128, k_stride_t=2 * 128, k_stride_h=128,
+                v_stride_t=2 * 128, v_stride_h=128, rel_stride_t=0, rel_stride_h=128,
+                out_stride_t=8 * 128, out_stride_h=128, softmax_scale=1 / 128,
+                qkv_dtype=_abi.IFA4_BF16, rel_dtype=_abi.IFA4_FP32)
+    base.update(kw)
+    return _abi.make_args(**base)
+
+
+def _validate(**kw):
+    return _abi.lib().ifa4_validate(ctypes.byref(_good(**kw)))
+
+
+@pytest.mark.parametrize("kw,expect", [
+    ({}, _abi.IFA4_OK),
+    ({"head_dim": 64, "q_stride_h": 64, "k_stride_h": 64, "v_stride_h": 64, "out_stride_h": 64},
+     _abi.IFA4_OK),
+    ({"qkv_dtype": _abi.IFA4_FP16, "rel_dtype": _abi.IFA4_BF16}, _abi.IFA4_OK),
+    ({"batch": 0, "q": 0, "k": 0}, _abi.IFA4_OK),  # empty batch: nothing is touched
+    ({"q": 0}, _abi.IFA4_EINVAL),
+    ({"cu_seqlens_k": 0}, _abi.IFA4_EINVAL),
+    ({"rel": 0}, _abi.IFA4_EINVAL),
+    ({"rel": 0, "rel_extent": 0}, _abi.IFA4_OK),  # no bias at all
+    ({"n_heads": 6, "kv_heads": 4}, _abi.IFA4_EINVAL),
+    ({"kv_heads": 0}, _abi.IFA4_EINVAL),
+    ({"rel_width": 64}, _abi.IFA4_EINVAL),
+    ({"window_left": -2}, _abi.IFA4_EINVAL),
+    ({"causal": 2}, _abi.IFA4_EINVAL),
+    ({"qkv_dtype": 7}, _abi.IFA4_EINVAL),
+    ({"max_seqlen_q": -1}, _abi.IFA4_EINVAL),
+    ({"q_stride_t": -8}, _abi.IFA4_EINVAL),
+    ({"softmax_scale": float("nan")}, _abi.IFA4_EINVAL),
+    ({"head_dim": 96}, _abi.IFA4_EUNSUPPORTED),
+    ({"qkv_dtype": _abi.IFA4_FP32}, _abi.IFA4_EUNSUPPORTED),
+    ({"softmax_scale": -0.5}, _abi.IFA4_EUNSUPPORTED),
+    ({"q": _P + 8}, _abi.IFA4_EUNSUPPORTED),          # 16-byte loads need alignment
+    ({"k_stride_t": 2 * 128 + 4}, _abi.IFA4_EUNSUPPORTED),
+    ({"lse": 9 * _P, "lse_stride_h": 64}, _abi.IFA4_EINVAL),  # lse rows overlap
+    ({"lse": 9 * _P, "lse_stride_h": 128}, _abi.IFA4_OK),
+])
+def test_validate(kw, expect):
+    assert _validate(**kw) == expect
+
+
+def test_launch_entry_points_reject_bad_args_before_any_launch():
+    lib = _abi.lib()
+    bad = _good(head_dim=96)
+    assert lib.ifa4_prefill_fwd(ctypes.byref(bad), None) == _abi.IFA4_EUNSUPPORTED
+    assert lib.ifa4_decode_fwd(ctypes.byref(bad), None, 0, None) == _abi.IFA4_EUNSUPPORTED
+    assert lib.ifa4_prefill_fwd(None, None) == _abi.IFA4_EINVAL
+
+
+def test_decode_workspace_and_contract():
+    lib = _abi.lib()
+    a = _good(batch=64, total_q=64, max_seqlen_q=1, max_seqlen_k=16384, total_k=600000,
+              causal=0)
+    ws = lib.ifa4_decode_workspace_bytes(ctypes.byref(a))
+    # causal decode sees key 0 only (top-left alignment): one split suffices
+    a_causal = _good(batch=64, total_q=64, max_seqlen_q=1, max_seqlen_k=16384, causal=1)
+    assert lib.ifa4_decode_workspace_bytes(ctypes.byref(a_causal)) < ws
+    tile = _abi.Ifa4Tile()
+    assert lib.ifa4_decode_tile(ctypes.byref(a), ctypes.byref(tile)) == _abi.IFA4_OK
+    splits = -(-16384 // tile.kv_chunk)
+    assert ws >= 64 * 8 * splits * (128 + 1) * 4
+    # missing / small workspace is reported, nothing launched
+    assert lib.ifa4_decode_fwd(ctypes.byref(a), None, 0, None) == _abi.IFA4_EWORKSPACE
+    assert lib.ifa4_decode_fwd(ctypes.byref(a), 256, ws - 1, None) == _abi.IFA4_EWORKSPACE
+    # decode needs one query per sequence
+    b = _good(batch=4, total_q=5, max_seqlen_q=2)
+    assert lib.ifa4_decode_workspace_bytes(ctypes.byref(b)) == 0
+    assert lib.ifa4_decode_fwd(ctypes.byref(b), 256, 1 << 30, None) == _abi.IFA4_EINVAL
+    # GQA groups above 16 are not served by the decode kernels
+    c = _good(batch=2, total_q=2, n_heads=32, kv_heads=1, max_seqlen_q=1)
+    assert lib.ifa4_decode_fwd(ctypes.byref(c), 256, 1 << 30, None) == _abi.IFA4_EUNSUPPORTED
+
+
+def test_tile_table_view():
+    t = _abi.prefill_tile(128)
+    assert (t.block_q, t.block_k) == (128, 64)
+    cfg = autotune_configs.get_preset(4096)
+    assert cfg == {"BLOCK_Q": t.block_q, "BLOCK_K": t.block_k, "num_warps": t.waves,
+                   "num_stages": t.stages}
+    assert "gfx950" in autotune_configs.PRESETS
+    assert autotune_configs._detect_arch().startswith("gfx")
+
+
+def _needed_tiles(lens_q, lens_k, causal, window, bq, bk):
+    """KV tiles holding at least one visible pair, per query tile (brute force
+    over the visibility mask of the reference semantics)."""
+    n = 0
+    for lq, lk in zip(lens_q, lens_k):
+        i = torch.arange(lq).unsqueeze(1)
+        j = torch.arange(lk).unsqueeze(0)
+        vis = torch.ones(lq, lk, dtype=torch.bool)
+        if causal:
+            vis &= i >= j
+        if window >= 0:
+            vis &= (i - j) <= window
+        for q0 in range(0, lq, bq):
+            cols = vis[q0:q0 + bq].any(0)
+            for k0 in range(0, lk, bk):
+                n += bool(cols[k0:k0 + bk].any())
+    return n
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_pruning_visits_exactly_the_tiles_with_visible_pairs(seed):
+    g = torch.Generator().manual_seed(seed)
+    batch = 3
+    lens_q = torch.randint(1, 400, (batch,), generator=g).tolist()
+    extra = torch.randint(0, 300, (batch,), generator=g).tolist()
+    lens_k = [a + b for a, b in zip(lens_q, extra)]
+    window = [-1, 63, 5, 200, -1, 0][seed]
+    causal = seed != 4
+    cu_q = [0] + list(torch.tensor(lens_q).cumsum(0).tolist())
+    cu_k = [0] + list(torch.tensor(lens_k).cumsum(0).tolist())
+    t = _abi.prefill_tile(128)
+    visited, total = _abi.count_tiles(cu_q, cu_k, 1, causal=causal, window_left=window)
+    need = _needed_tiles(lens_q, lens_k, causal, window, t.block_q, t.block_k)
+    assert visited == need
+    all_tiles, _ = _abi.count_tiles(cu_q, cu_k, 1, causal=causal, window_left=window,
+                                    no_prune=True)
+    assert all_tiles == total
+
+
+def test_chunked_window_workload_tile_counts():
+    """128 new tokens over a 384-key cache, window 63: 2 of 6 KV tiles per
+    query tile are visited."""
+    cu_q = [128 * b for b in range(17)]
+    cu_k = [384 * b for b in range(17)]
+    visited, total = _abi.count_tiles(cu_q, cu_k, 8, causal=True, window_left=63)
+    assert (visited, total) == (16 * 8 * 2, 16 * 8 * 6)
