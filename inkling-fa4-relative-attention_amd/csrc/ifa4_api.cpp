@@ -60,6 +60,21 @@ int32_t check_args(const ifa4_args* a) {
     return IFA4_EUNSUPPORTED;
   if (a->rel != nullptr && !aligned(a->rel, a->rel_dtype == IFA4_FP32 ? 4 : 2))
     return IFA4_EINVAL;
+  // Kernels address one sequence of one head through a buffer resource with
+  // 32-bit offsets and read rows past the sequence end as zero: token rows
+  // must not overlap, and a sequence's rows must span less than 2 GiB.
+  if (a->q_stride_t < a->head_dim || a->k_stride_t < a->head_dim ||
+      a->v_stride_t < a->head_dim)
+    return IFA4_EUNSUPPORTED;
+  if (a->rel_stride_t != 0 && a->rel_stride_t < a->rel_width) return IFA4_EUNSUPPORTED;
+  const int64_t rel_esize = a->rel_dtype == IFA4_FP32 ? 4 : 2;
+  const int64_t kLimit = int64_t(1) << 31;
+  const int64_t kpad = 128;  // rows a tile may read past the end
+  if ((a->max_seqlen_q + kpad) * a->q_stride_t * 2 >= kLimit ||
+      (a->max_seqlen_k + kpad) * a->k_stride_t * 2 >= kLimit ||
+      (a->max_seqlen_k + kpad) * a->v_stride_t * 2 >= kLimit ||
+      ((a->max_seqlen_q + kpad) * a->rel_stride_t + a->rel_width) * rel_esize >= kLimit)
+    return IFA4_EUNSUPPORTED;
   return IFA4_OK;
 }
 
@@ -88,6 +103,7 @@ ifa4::PrefillParams make_prefill_params(const ifa4_args* a) {
   p.n_heads = a->n_heads;
   p.group = a->n_heads / a->kv_heads;
   p.rel_extent = a->rel_extent;
+  p.rel_width = a->rel_width;
   p.window_left = a->window_left;
   p.causal = a->causal;
   p.no_prune = (a->flags & IFA4_FLAG_NO_PRUNE) ? 1 : 0;

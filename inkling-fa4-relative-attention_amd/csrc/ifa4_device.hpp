@@ -44,6 +44,12 @@ template <> struct Elem<Bf16Tag> {
     bf16x2_t v = {(__bf16)lo, (__bf16)hi};
     return __builtin_bit_cast(uint32_t, v);
   }
+  // acc + lo(w) + hi(w), one v_dot2 (sum of a packed pair)
+  static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), one, acc, false);
+  }
   static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
   static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
   static __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
@@ -60,6 +66,11 @@ template <> struct Elem<F16Tag> {
     typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
     f16x2_t v = {(_Float16)lo, (_Float16)hi};
     return __builtin_bit_cast(uint32_t, v);
+  }
+  static __device__ __forceinline__ float sum2(uint32_t w, float acc) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), one, acc, false);
   }
   static __device__ __forceinline__ float lo(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
@@ -105,5 +116,46 @@ __device__ __forceinline__ bool wave_any(bool p) {
 __device__ __forceinline__ u32x4_t ld_global_16(const void* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
 }
+
+// ---- buffer addressing -------------------------------------------------------------
+// A buffer resource covers [base, base + bytes); a load whose offset lies past
+// the end returns zeros instead of touching memory.  The kernels use this for
+// ragged tails (no branches around loads) and 32-bit per-sequence offsets.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // offset past any resource used here
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4_t buf_load_16(rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load_4(rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load_2(rsrc_t r, uint32_t byte_off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)byte_off, 0, 0);
+}
+
+// Bias element types: storage size and conversion of the loaded bits to fp32.
+struct RelF32 {
+  static constexpr int kBytes = 4;
+  static __device__ __forceinline__ float load(rsrc_t r, uint32_t off) {
+    return __uint_as_float(buf_load_4(r, off));
+  }
+};
+struct RelBf16 {
+  static constexpr int kBytes = 2;
+  static __device__ __forceinline__ float load(rsrc_t r, uint32_t off) {
+    return __uint_as_float(buf_load_2(r, off) << 16);
+  }
+};
+struct RelF16 {
+  static constexpr int kBytes = 2;
+  static __device__ __forceinline__ float load(rsrc_t r, uint32_t off) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)buf_load_2(r, off));
+  }
+};
 
 }  // namespace ifa4

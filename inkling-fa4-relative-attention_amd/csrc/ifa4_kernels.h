@@ -21,6 +21,7 @@ struct PrefillParams {
   int32_t n_heads;
   int32_t group;        // n_heads / kv_heads
   int32_t rel_extent;
+  int32_t rel_width;    // last dim of rel (>= rel_extent)
   int32_t window_left;  // -1: none
   int32_t causal;
   int32_t no_prune;

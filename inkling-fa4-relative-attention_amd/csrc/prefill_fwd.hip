@@ -8,7 +8,8 @@
 // Work decomposition.  A workgroup of 4 waves owns BLOCK_Q = 128 query rows of
 // one (sequence, head); wave w owns rows 32w .. 32w+31.  K/V tiles of BLOCK_K =
 // 64 keys are staged in LDS (double buffered, register prefetch of the next
-// tile while the current one is computed).
+// tile while the current one is computed).  Two workgroups share a CU (two
+// waves per SIMD), so one wave's softmax overlaps the other's matrix products.
 //
 // Score layout.  Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16:
 // A = K rows from LDS, B = Q held in registers for the whole KV loop.  In the
@@ -20,15 +21,21 @@
 // 16-key group permuted (bits 2 and 3 swapped) so every A operand of the PV
 // product is one 16-byte LDS read.
 //
+// Memory access.  Q/K/V rows and bias values are read with buffer loads over
+// per-(sequence, head) resources: rows past the sequence end fall outside the
+// resource and read as zero, so ragged tails need no branches and offsets are
+// 32-bit.
+//
 // Softmax.  exp2 with softmax_scale*log2(e) folded into one FMA; the bias is
 // pre-multiplied by log2(e).  The running max is only raised when it grows by
 // more than 2^8 (deferred rescale), which keeps the result exact and skips the
-// O rescale on most tiles.
+// O rescale on most tiles.  Row sums accumulate the fp32 P (summing the
+// rounded 16-bit P instead would cost the LSE up to 2^-9 relative on short rows).
 //
 // Tile classes per (wave, KV tile): fully masked -> skipped (causal: keys after
 // the wave's last row; window: keys left of the window); edge (diagonal, window
 // boundary, KV tail, or within the relative-bias band 0 <= dist < rel_extent)
-// -> per-element mask + bias gather; interior -> plain flash attention.
+// -> per-element key-range mask + bias gather; interior -> plain flash attention.
 #include "ifa4_device.hpp"
 #include "ifa4_kernels.h"
 
@@ -47,17 +54,22 @@ struct PrefillLds {
   static constexpr int kElems = kBlockK * kPitch;
   static constexpr int vElems = D * vPitch;
   static constexpr int stage = kElems + vElems;  // 16-bit elements per stage
-  static constexpr int bytes = 2 * stage * 2;    // two stages
 };
 
-// LDS position of key `kk` (0..63) inside a V^T row: bits 2 and 3 swapped, so
-// the 8 keys one lane needs for a 16-key PV step are contiguous.
+// LDS position of key `kk` inside a V^T row: bits 2 and 3 swapped, so the 8
+// keys one lane needs for a 16-key PV step are contiguous.
 __device__ __forceinline__ int vt_pos(int kk) {
   return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
 }
 
-template <int D, typename Tag>
-__global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) {
+// Bytes a resource over `rows` rows of `stride` elements (row length d) spans.
+__device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int d, int esize) {
+  return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + d) * esize) : 0u;
+}
+
+template <int D, typename Tag, typename Rel>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_fwd_kernel(PrefillParams p) {
   using E = Elem<Tag>;
   using L = PrefillLds<D>;
   constexpr int kKChunks = D / 8;                         // 16-byte chunks per K row
@@ -85,12 +97,25 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
   const int kvh = head / p.group;
   const int delta = lq - lk;
   const int wl = p.window_left;
+  const int rext = p.rel_extent;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int col = lane & 31;   // query column of this lane
   const int half = lane >> 5;  // 0 / 1
+
+  // ---- per-(sequence, head) buffer resources --------------------------------------
+  const uint16_t* q_base = static_cast<const uint16_t*>(p.q) + (int64_t)qs * p.q_st +
+                           (int64_t)head * p.q_sh;
+  const uint16_t* k_base = static_cast<const uint16_t*>(p.k) + (int64_t)ks * p.k_st +
+                           (int64_t)kvh * p.k_sh;
+  const uint16_t* v_base = static_cast<const uint16_t*>(p.v) + (int64_t)ks * p.v_st +
+                           (int64_t)kvh * p.v_sh;
+  const rsrc_t rq = make_rsrc(q_base, span_bytes(lq, p.q_st, D, 2));
+  const rsrc_t rk = make_rsrc(k_base, span_bytes(lk, p.k_st, D, 2));
+  const rsrc_t rv = make_rsrc(v_base, span_bytes(lk, p.v_st, D, 2));
+  const uint32_t k_row = (uint32_t)p.k_st * 2, v_row = (uint32_t)p.v_st * 2;
 
   // ---- key range of the workgroup (tile pruning) ---------------------------
   const int q_hi = min(q0 + kBlockQ, lq);  // exclusive
@@ -103,9 +128,9 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
   const int kt_end = kend > kbeg ? (kend + kBlockK - 1) / kBlockK : kt_beg;
 
   // ---- per-wave rows ---------------------------------------------------------
-  const int qa = q0 + 32 * wave;                  // first row of the wave (local)
-  const int wrows = max(0, min(32, lq - qa));     // valid rows of the wave
-  const int qi = qa + col;                        // this lane's query (local)
+  const int qa = q0 + 32 * wave;               // first row of the wave (local)
+  const int wrows = max(0, min(32, lq - qa));  // valid rows of the wave
+  const int qi = qa + col;                     // this lane's query (local)
   const bool row_ok = qi < lq;
   int wkend = lk, wkbeg = 0;
   if (!p.no_prune) {
@@ -114,17 +139,10 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
   }
 
   // ---- Q fragment (B operand), kept for the whole loop -----------------------
-  const uint16_t* qbase = static_cast<const uint16_t*>(p.q);
   u32x4_t qf[kKSteps];
 #pragma unroll
-  for (int kk = 0; kk < kKSteps; ++kk) {
-    if (row_ok) {
-      qf[kk] = ld_global_16(qbase + (int64_t)(qs + qi) * p.q_st + (int64_t)head * p.q_sh +
-                            16 * kk + 8 * half);
-    } else {
-      qf[kk] = u32x4_t{0, 0, 0, 0};
-    }
-  }
+  for (int kk = 0; kk < kKSteps; ++kk)
+    qf[kk] = buf_load_16(rq, (uint32_t)(qi * p.q_st + 16 * kk + 8 * half) * 2);
 
   const float c2 = p.scale_log2;  // softmax_scale * log2(e)
   float m_run = -INFINITY;         // running max (log2 domain), same in both halves
@@ -134,10 +152,6 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
   for (int db = 0; db < kDBlocks; ++db) o[db] = f32x16_t{};
 
   // ---- K/V tile loader (global -> registers -> LDS) ---------------------------
-  const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (int64_t)ks * p.k_st +
-                          (int64_t)kvh * p.k_sh;
-  const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (int64_t)ks * p.v_st +
-                          (int64_t)kvh * p.v_sh;
   u32x4_t kreg[kKItems];
   u32x4_t vreg[4];
   const bool v_loader = tid < kVItems;
@@ -151,17 +165,12 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
       const int item = tid + r * kThreads;
       const int row = item / kKChunks;
       const int ch = item % kKChunks;
-      const int key = kb + row;
-      kreg[r] = key < lk ? ld_global_16(kbase + (int64_t)key * p.k_st + 8 * ch)
-                         : u32x4_t{0, 0, 0, 0};
+      kreg[r] = buf_load_16(rk, (uint32_t)(kb + row) * k_row + 16 * ch);
     }
     if (v_loader) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kb + 4 * v_kg + r;
-        vreg[r] = key < lk ? ld_global_16(vbase + (int64_t)key * p.v_st + 8 * v_dc)
-                           : u32x4_t{0, 0, 0, 0};
-      }
+      for (int r = 0; r < 4; ++r)
+        vreg[r] = buf_load_16(rv, (uint32_t)(kb + 4 * v_kg + r) * v_row + 16 * v_dc);
     }
   };
   auto store_tile = [&](int buf) {
@@ -191,8 +200,12 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
     }
   };
 
-  const float rel_l2 = kLog2e;
-  const int rext = p.rel_extent;
+  // Bias resource: the (sequence, head) rows of the bias; this lane reads its row.
+  const rsrc_t rrel = make_rsrc(
+      static_cast<const char*>(p.rel) + ((int64_t)qs * p.rel_st + (int64_t)head * p.rel_sh) *
+                                            Rel::kBytes,
+      span_bytes(lq, p.rel_st, p.rel_width, Rel::kBytes));
+  const uint32_t rel_row_off = (uint32_t)(qi * p.rel_st) * Rel::kBytes;
 
   if (kt_beg < kt_end) load_tile(kt_beg);
   for (int kt = kt_beg; kt < kt_end; ++kt) {
@@ -209,8 +222,8 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
     const int jmin = kb, jmax = kb + kBlockK - 1;
     const bool need_mask = jmax >= lk || (p.causal && jmax > imin) ||
                            (wl >= 0 && imax - jmin > wl);
-    const bool has_bias = (imax + delta - jmin >= 0) && (imin + delta - jmax <= rext - 1);
-    const bool edge = need_mask || has_bias;
+    const bool has_bias =
+        rext > 0 && (imax + delta - jmin >= 0) && (imin + delta - jmax <= rext - 1);
 
     const uint16_t* kl = lds + buf * L::stage;
     const uint16_t* vl = kl + L::kElems;
@@ -229,26 +242,40 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
     }
 
     // ---- logits (log2 domain) and tile max ---------------------------------------
+    // Element (blk, e) of this lane is tile-local key 32*blk + 8*(e>>2) + (e&3)
+    // + 4*half; `kc` below drops the lane term, which is folded into the bounds.
     float sc;  // factor applied inside the exponent FMA
     float mx = -INFINITY;
-    if (edge) {
+    if (need_mask || has_bias) {
       sc = 1.f;
-      const int64_t rrow = (int64_t)(qs + qi) * p.rel_st + (int64_t)head * p.rel_sh;
+      int hi = lk - 1 - kb;
+      if (p.causal) hi = min(hi, qi - kb);
+      if (!row_ok) hi = -1;
+      const int lo = wl >= 0 ? qi - wl - kb : -1;
+      const int hi_h = hi - 4 * half, lo_h = lo - 4 * half;
+      const int dbase = qi + delta - kb - 4 * half;  // dist = dbase - kc
+      float bias[kBlockK / 2];
+      if (has_bias) {
+#pragma unroll
+        for (int blk = 0; blk < kBlockK / 32; ++blk)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
+            const int dist = dbase - kc;
+            const uint32_t off = (uint32_t)dist < (uint32_t)rext
+                                     ? rel_row_off + (uint32_t)dist * Rel::kBytes
+                                     : kOutOfRange;
+            bias[16 * blk + e] = Rel::load(rrel, off);
+          }
+      }
 #pragma unroll
       for (int blk = 0; blk < kBlockK / 32; ++blk) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          const int key = kb + 32 * blk + 8 * (e >> 2) + 4 * half + (e & 3);
-          bool vis = row_ok && key < lk;
-          if (p.causal) vis = vis && qi >= key;
-          if (wl >= 0) vis = vis && (qi - key) <= wl;
+          const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
           float x = s[blk][e] * c2;
-          if (has_bias) {
-            const int dist = qi + delta - key;
-            if (vis && dist >= 0 && dist < rext)
-              x += load_rel(p.rel, rrow + dist, p.rel_dtype) * rel_l2;
-          }
-          x = vis ? x : -INFINITY;
+          if (has_bias) x = fmaf(bias[16 * blk + e], kLog2e, x);
+          x = (kc >= lo_h && kc <= hi_h) ? x : -INFINITY;
           s[blk][e] = x;
           mx = fmaxf(mx, x);
         }
@@ -278,21 +305,19 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
 
-    // ---- P = exp2(x - m), row sum, pack to the PV B operand -------------------------
+    // ---- P = exp2(x - m), packed to the PV B operand, row sum ----------------------
     u32x4_t pb[kBlockK / 16];
-    float lsum = 0.f;
 #pragma unroll
     for (int t = 0; t < kBlockK / 16; ++t) {
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         pv[e] = fast_exp2(fmaf(s[t >> 1][8 * (t & 1) + e], sc, -m_use));
-        lsum += pv[e];
+        l_run += pv[e];
       }
       pb[t] = u32x4_t{E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
                       E::pack2(pv[6], pv[7])};
     }
-    l_run += lsum;
 
     // ---- O^T += V^T P^T ----------------------------------------------------------
 #pragma unroll
@@ -329,14 +354,23 @@ __global__ __launch_bounds__(kThreads) void prefill_fwd_kernel(PrefillParams p) 
   }
 }
 
-template <int D, typename Tag>
+template <int D, typename Tag, typename Rel>
 hipError_t launch_prefill_t(const PrefillParams& p, hipStream_t stream) {
   const int per_tile = p.n_heads * p.batch;
   const int64_t blocks = (int64_t)p.n_qtiles * per_tile;
   if (blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL((prefill_fwd_kernel<D, Tag>), dim3((unsigned)blocks), dim3(kThreads), 0,
-                     stream, p);
+  hipLaunchKernelGGL((prefill_fwd_kernel<D, Tag, Rel>), dim3((unsigned)blocks), dim3(kThreads),
+                     0, stream, p);
   return hipGetLastError();
+}
+
+template <int D, typename Tag>
+hipError_t launch_prefill_rel(const PrefillParams& p, hipStream_t stream) {
+  switch (p.rel_dtype) {
+    case 0: return launch_prefill_t<D, Tag, RelBf16>(p, stream);
+    case 1: return launch_prefill_t<D, Tag, RelF16>(p, stream);
+    default: return launch_prefill_t<D, Tag, RelF32>(p, stream);
+  }
 }
 
 }  // namespace
@@ -348,11 +382,11 @@ int prefill_waves() { return kWaves; }
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, int qkv_dtype,
                           hipStream_t stream) {
   if (head_dim == 128) {
-    return qkv_dtype == 0 ? launch_prefill_t<128, Bf16Tag>(p, stream)
-                          : launch_prefill_t<128, F16Tag>(p, stream);
+    return qkv_dtype == 0 ? launch_prefill_rel<128, Bf16Tag>(p, stream)
+                          : launch_prefill_rel<128, F16Tag>(p, stream);
   }
-  return qkv_dtype == 0 ? launch_prefill_t<64, Bf16Tag>(p, stream)
-                        : launch_prefill_t<64, F16Tag>(p, stream);
+  return qkv_dtype == 0 ? launch_prefill_rel<64, Bf16Tag>(p, stream)
+                        : launch_prefill_rel<64, F16Tag>(p, stream);
 }
 
 }  // namespace ifa4
