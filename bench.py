@@ -142,29 +142,88 @@ def copy_bandwidth():
     return 2 * n / (ms * 1e-3) / 1e9
 
 
-def cpu_baseline(case):
-    """fp32 CPU oracle on one sequence of the headline batch (all heads)."""
+def cpu_baseline(case, budget_s=10.0):
+    """fp32 CPU oracle on whole sequences of the headline batch (all heads),
+    one after another until `budget_s` seconds have elapsed or the batch is done."""
     import torch
     from oracle import ref_rel_attn
 
-    threads = os.cpu_count() or 1
+    try:
+        threads = len(os.sched_getaffinity(0))
+    except AttributeError:
+        threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     cq, ck = case.cu_q.tolist(), case.cu_k.tolist()
-    q = case.q[cq[0]:cq[1]]
-    k = case.k[ck[0]:ck[1]]
-    v = case.v[ck[0]:ck[1]]
-    rel = case.rel[cq[0]:cq[1]]
-    lq = cq[1] - cq[0]
-    cu = torch.tensor([0, lq], dtype=torch.int32)
-    pairs = lq * (lq + 1) // 2 * q.shape[1]
-    flops = 4.0 * q.shape[2] * pairs
-    t0 = time.perf_counter()
-    ref_rel_attn(q, k, v, rel, cu, cu, case.scale, case.rel_extent, causal=True)
+    flops, done, t0 = 0.0, 0, time.perf_counter()
+    for b in range(len(cq) - 1):
+        q = case.q[cq[b]:cq[b + 1]]
+        k = case.k[ck[b]:ck[b + 1]]
+        v = case.v[ck[b]:ck[b + 1]]
+        rel = case.rel[cq[b]:cq[b + 1]]
+        lq = cq[b + 1] - cq[b]
+        cu = torch.tensor([0, lq], dtype=torch.int32)
+        ref_rel_attn(q, k, v, rel, cu, cu, case.scale, case.rel_extent, causal=True)
+        flops += 4.0 * q.shape[2] * (lq * (lq + 1) // 2) * q.shape[1]
+        done += 1
+        log(f"cpu baseline: sequence {b} done ({time.perf_counter() - t0:.1f} s)")
+        if time.perf_counter() - t0 >= budget_s:
+            break
     dt = time.perf_counter() - t0
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port", "seconds": dt,
-            "sample": f"sequence 0 of the batch ({lq} tokens, all {q.shape[1]} heads), "
-                      f"fp32 oracle on the host CPU, os.cpu_count()={threads}"}
+            "kind": "port", "seconds": round(dt, 2),
+            "sample": f"{done} of {len(cq) - 1} sequences of the headline batch "
+                      f"({cq[1] - cq[0]} tokens, all {case.q.shape[1]} heads each), "
+                      "fp32 oracle (dense per sequence/head) on the host CPU"}
+
+
+def traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE KiB per dispatch, each scaled by the
+    factor the same counter reads for a device copy of known size)."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        k = t["kernels"][kernel]
+        cal = t["copy_calibration"]
+        return round(1024 * (k["fetch_kib"] * cal["fetch_factor"] +
+                             k["write_kib"] * cal["write_factor"]))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_loop(n_bytes=256 << 20, reps=5):
+    """Device copies of a known size, for calibrating FETCH_SIZE/WRITE_SIZE."""
+    import torch
+
+    a = torch.ones(n_bytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"copied {reps} x {n_bytes} bytes")
+
+
+def summarize(db_path):
+    """Print per-kernel dispatch statistics and per-dispatch counter averages
+    from a rocprofv3 output database (SQLite)."""
+    import sqlite3
+
+    con = sqlite3.connect(db_path)
+    print(f"profile: {db_path}")
+    print("| kernel | calls | avg us | total us | % |")
+    print("|---|---|---|---|---|")
+    for name, n, tot, avg, pct in con.execute(
+            "select name, total_calls, total_duration, average, percentage from top_kernels"):
+        print(f"| {name} | {n} | {avg:.3f} | {tot:.1f} | {pct:.1f} |")
+    rows = list(con.execute("select kernel_name, counter_name, avg(value), count(*) "
+                            "from counters_collection group by kernel_name, counter_name"))
+    if rows:
+        print()
+        print("| kernel | counter | per-dispatch avg | dispatches |")
+        print("|---|---|---|---|")
+        for k, cn, v, n in rows:
+            print(f"| {k} | {cn} | {v:.6g} | {n} |")
 
 
 def main():
@@ -176,7 +235,14 @@ def main():
     ap.add_argument("--only", choices=["all", "prefill", "decode"], default="all")
     ap.add_argument("--seq", type=int, default=4096)
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--summarize", metavar="DB",
+                    help="print a rocprofv3 output database as markdown tables and exit")
+    ap.add_argument("--copy-only", action="store_true",
+                    help="only run device copies of a known size (counter calibration)")
     args = ap.parse_args()
+    if args.summarize:
+        summarize(args.summarize)
+        return 0
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
@@ -190,6 +256,9 @@ def main():
         return 1
     dev_name = torch.cuda.get_device_name(0)
     log(f"device {dev_name}")
+    if args.copy_only:
+        copy_loop()
+        return 0
 
     result = {
         "metric": "prefill ms + TFLOPS @seq4096 Hq8/Hkv2 d128; decode KV GB/s; % roofline",
@@ -213,7 +282,7 @@ def main():
                               "achieved": round(pre["tflops"], 2),
                               "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                               "frac": round(pre["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
-                              "traffic": None}
+                              "traffic": traffic("prefill_fwd_kernel")}
         if not args.no_sweep:
             sweep = {}
             for s in (1024, 2048, 8192):
@@ -233,7 +302,7 @@ def main():
                                                 "achieved": round(dec["gbps"], 1),
                                                 "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                                                 "frac": round(dec["frac_of_peak"], 4),
-                                                "traffic": None}}
+                                                "traffic": traffic("decode_split_kernel")}}
         if result["value"] is None:
             result["value"] = round(dec["gbps"], 1)
             result["unit"] = "GB/s"

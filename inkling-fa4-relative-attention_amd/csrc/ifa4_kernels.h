@@ -27,6 +27,7 @@ struct PrefillParams {
   int32_t no_prune;
   int32_t rel_dtype;    // 0 bf16, 1 fp16, 2 fp32
   int32_t n_qtiles;     // ceil(max_seqlen_q / block_q)
+  int32_t xcd_pairs;    // (sequence, kv head) pairs per XCD in the XCD-aware order, or 0
   float scale_log2;     // softmax_scale * log2(e)
 };
 
