@@ -22,7 +22,7 @@
 // It writes the normalised partial o and its log2-sum-exp to the workspace.
 //
 // Pass 2 (decode_combine_kernel): per (head, sequence) merge of the valid
-// splits by log-sum-exp (wave-parallel max/sum, independent partial loads);
+// splits by log-sum-exp (four waves share the splits, wave-parallel max/sum);
 // writes out (q dtype) and lse (natural log).
 #include "ifa4_device.hpp"
 #include "ifa4_kernels.h"
@@ -269,10 +269,15 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+constexpr int kCombineWaves = 4;
+
+// One workgroup per (head, sequence); wave w merges splits w, w+4, ... with
+// independent loads in flight, the four partial sums meet in LDS.
 template <int D, typename Tag>
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(DecodeParams p) {
   using E = Elem<Tag>;
   constexpr int kPer = D / 64;  // d values per lane
+  __shared__ float part[kCombineWaves - 1][64 * kPer];
   const int head = blockIdx.x;
   const int seq = blockIdx.y;
   const int qs = p.cu_q[seq];
@@ -283,11 +288,13 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   // Splits pass 1 wrote for this sequence (never more than were launched, even
   // if a length exceeds the max_seqlen_k the grid was sized with).
   const int ns = min(kend > 0 ? (kend + p.chunk - 1) / p.chunk : 0, p.n_splits);
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)seq * p.n_heads + head;
   const float* lse_s = p.ws_lse + row * p.n_splits;
   const float* o_s = p.ws_o + row * p.n_splits * D + kPer * lane;
 
+  // Every wave computes the max and the weight sum over all splits.
   float m = -INFINITY;
   for (int s = lane; s < ns; s += 64) m = fmaxf(m, lse_s[s]);
   m = wave_max(m);
@@ -299,27 +306,23 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   float acc[kPer];
 #pragma unroll
   for (int e = 0; e < kPer; ++e) acc[e] = 0.f;
-  int s = 0;
-  for (; s + 4 <= ns; s += 4) {
-    float w[4], v[4][kPer];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      w[u] = lse_s[s + u];
-#pragma unroll
-      for (int e = 0; e < kPer; ++e) v[u][e] = o_s[(int64_t)(s + u) * D + e];
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float wu = fast_exp2(w[u] - m_use);
-#pragma unroll
-      for (int e = 0; e < kPer; ++e) acc[e] = fmaf(wu, v[u][e], acc[e]);
-    }
-  }
-  for (; s < ns; ++s) {
+#pragma unroll 8
+  for (int s = wave; s < ns; s += kCombineWaves) {
     const float wu = fast_exp2(lse_s[s] - m_use);
 #pragma unroll
     for (int e = 0; e < kPer; ++e) acc[e] = fmaf(wu, o_s[(int64_t)s * D + e], acc[e]);
   }
+  if (wave > 0) {
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) part[wave - 1][kPer * lane + e] = acc[e];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < kCombineWaves - 1; ++w)
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) acc[e] += part[w][kPer * lane + e];
+
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
   uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)qs * p.o_st + (int64_t)head * p.o_sh +
                   kPer * lane;
@@ -340,8 +343,8 @@ hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
                      dim3(64), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((decode_combine_kernel<D, Tag>), dim3(p.n_heads, p.batch), dim3(64), 0,
-                     stream, p);
+  hipLaunchKernelGGL((decode_combine_kernel<D, Tag>), dim3(p.n_heads, p.batch),
+                     dim3(64 * kCombineWaves), 0, stream, p);
   return hipGetLastError();
 }
 

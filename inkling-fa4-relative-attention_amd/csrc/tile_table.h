@@ -30,8 +30,11 @@ constexpr PrefillTileEntry kPrefillTiles[] = {
     {128, 128, 64, 4, 2},
 };
 
-constexpr int32_t kDecodeChunks[] = {512, 256, 128, 64};
-constexpr int64_t kDecodeTargetWaves = 2048;
+#ifndef IFA4_DECODE_TARGET_WAVES
+#define IFA4_DECODE_TARGET_WAVES 8192
+#endif
+constexpr int32_t kDecodeChunks[] = {1024, 512, 256, 128, 64};
+constexpr int64_t kDecodeTargetWaves = IFA4_DECODE_TARGET_WAVES;
 
 inline int32_t decode_chunk_for(int64_t batch, int64_t kv_heads, int64_t max_seqlen_k) {
   for (int32_t c : kDecodeChunks) {
