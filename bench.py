@@ -44,11 +44,26 @@ def _ensure_built():
         __graft_entry__.build()
 
 
-def time_gpu(fn, steps, warmup):
-    """Average ms per call of `fn` over `steps` back-to-back calls, bracketed by
-    HIP events on the current stream (where the operator launches)."""
+def settle(fn, seconds=0.5):
+    """Run `fn` untimed for about `seconds` of wall time.  The GPU clock ramps
+    up over a few hundred ms of load; ten warmup calls of a 0.3 ms kernel are
+    not enough (the first timed window then runs ~12% slow)."""
     import torch
 
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
+def time_gpu(fn, steps, warmup):
+    """Average ms per call of `fn` over `steps` back-to-back calls, bracketed by
+    HIP events on the current stream (where the operator launches).  The
+    clocks are settled first, then `warmup` untimed calls run."""
+    import torch
+
+    settle(fn)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()

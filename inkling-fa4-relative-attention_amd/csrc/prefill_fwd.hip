@@ -5,11 +5,17 @@
 // with one launch over every (query tile, head, sequence) instead of one launch
 // per sequence (triton_kernel.py:94-106).
 //
-// Work decomposition.  A workgroup of 4 waves owns BLOCK_Q = 128 query rows of
-// one (sequence, head); wave w owns rows 32w .. 32w+31.  K/V tiles of BLOCK_K =
-// 64 keys are staged in LDS (double buffered, register prefetch of the next
-// tile while the current one is computed).  Two workgroups share a CU (two
-// waves per SIMD), so one wave's softmax overlaps the other's matrix products.
+// Work decomposition.  A workgroup owns BLOCK_Q = 128 query rows of one
+// (sequence, head).  Each wave owns NQB blocks of 32 rows.  K/V tiles of
+// BLOCK_K = 64 keys go from HBM straight into LDS with buffer_load ... lds
+// (no registers, no LDS store instructions); two LDS stages, the DMA of the
+// next tile is in flight while the current one is computed.  Two shapes:
+//   NQB = 2: 2 waves x 64 rows, 1 wave per SIMD with up to 512 registers;
+//            every K / V^T fragment read from LDS feeds two MFMAs, and the two
+//            independent row blocks let one block's softmax overlap the other
+//            block's matrix products inside the wave;
+//   NQB = 1: 4 waves x 32 rows, 2 waves per SIMD (<= 256 registers); the two
+//            workgroups on a CU interleave instead.
 //
 // Score layout.  Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16:
 // A = K rows from LDS, B = Q held in registers for the whole KV loop.  In the
@@ -17,9 +23,13 @@
 // 32-key block, so the row max/sum of the softmax are in-lane reductions plus
 // one exchange with lane l ^ 32, and P leaves the accumulator already in the
 // B-operand layout of the next product O^T = V^T P^T (no LDS round trip for P).
-// V is written to LDS transposed (V^T[d][key]) with the key order inside each
-// 16-key group permuted (bits 2 and 3 swapped) so every A operand of the PV
-// product is one 16-byte LDS read.
+// V stays row-major in LDS; the A operand of the PV product (V^T, 8 keys per
+// lane) is two ds_read_b64_tr_b16 transposing reads: within a 16-lane group,
+// source lane j pointing at V[k0 + j/4][d0 + 4(j%4)] returns to lane i the
+// four values V[k0 .. k0+3][d0 + i], which is exactly the key order of P.
+// LDS rows are stored with their 16-byte chunks XOR-swizzled by
+// f(row) = 4(row & 3) | ((row >> 2) & 3), so the 8-row K reads and the
+// 4-row transposing V reads each hit distinct banks.
 //
 // Memory access.  Q/K/V rows and bias values are read with buffer loads over
 // per-(sequence, head) resources: rows past the sequence end fall outside the
@@ -45,31 +55,56 @@
 #include "ifa4_kernels.h"
 
 #ifndef IFA4_PRIO
-#define IFA4_PRIO 0
+#define IFA4_PRIO 1
+#endif
+#ifndef IFA4_PREFILL_NQB
+#define IFA4_PREFILL_NQB 1
+#endif
+#ifndef IFA4_SCHED
+#define IFA4_SCHED 1
 #endif
 
 namespace ifa4 {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kBlockQ = 32 * kWaves;  // 128
+constexpr int kNqb = IFA4_PREFILL_NQB;           // 32-row query blocks per wave
+constexpr int kWaves = kNqb == 1 ? 4 : 2;        // waves per workgroup
+constexpr int kBlockQ = 32 * kNqb * kWaves;      // 128
 constexpr int kBlockK = 64;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kWavesPerSimd = kNqb == 1 ? 2 : 1;
+#ifndef IFA4_LOOK_K
+#define IFA4_LOOK_K 4
+#endif
+#ifndef IFA4_LOOK_V
+#define IFA4_LOOK_V 4
+#endif
+constexpr int kLookK = IFA4_LOOK_K;  // K fragment reads in flight ahead of the QK MFMAs
+constexpr int kLookV = IFA4_LOOK_V;  // V^T operand pairs in flight ahead of the PV MFMAs
 
+// One LDS stage: K tile then V tile, each [kBlockK][D] row-major, swizzled.
 template <int D>
-struct PrefillLds {
-  static constexpr int kPitch = D + 8;           // K row pitch (elements)
-  static constexpr int vPitch = kBlockK + 8;     // V^T row pitch (elements)
-  static constexpr int kElems = kBlockK * kPitch;
-  static constexpr int vElems = D * vPitch;
-  static constexpr int stage = kElems + vElems;  // 16-bit elements per stage
+struct PrefillStage {
+  static constexpr int kTile = kBlockK * D;              // 16-bit elements per tensor
+  static constexpr int kElems = 2 * kTile;
+  static constexpr int kChunks = D / 8;                  // 16-byte chunks per row
+  static constexpr int kRowsPerDma = 1024 / (2 * D);     // rows one wave DMA covers
+  static constexpr int kDmaPerTensor = kBlockK / kRowsPerDma;
+  static constexpr int kDmaPerWave = 2 * kDmaPerTensor / kWaves;
 };
 
-// LDS position of key `kk` inside a V^T row: bits 2 and 3 swapped, so the 8
-// keys one lane needs for a 16-key PV step are contiguous.
-__device__ __forceinline__ int vt_pos(int kk) {
-  return (kk & ~12) | ((kk & 4) << 1) | ((kk & 8) >> 1);
+// 16-byte chunk swizzle of an LDS row, kChunks = chunks per row (16 or 8).
+// Measured with the LDS bank-conflict counter on gfx950: zero conflicts for
+// both the 8-row K reads (ds_read_b128) and the 4-row transposing V reads
+// (ds_read_b64_tr_b16) at 16 chunks per row.
+template <int kChunks>
+__device__ __forceinline__ int swz(int row) {
+  return (((row & 3) << 2) | ((row >> 2) & 3)) & (kChunks - 1);
 }
+
+// s_waitcnt immediate: wait until at most n vector-memory operations of this
+// wave are outstanding (LDS/export counters left unconstrained).
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
 
 // Bytes a resource over `rows` rows of `stride` elements (row length d) spans.
 __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int d, int esize) {
@@ -77,17 +112,16 @@ __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int d, 
 }
 
 template <int D, typename Tag, typename Rel>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd,
+                                                                          kWavesPerSimd)))
 void prefill_fwd_kernel(PrefillParams p) {
   using E = Elem<Tag>;
-  using L = PrefillLds<D>;
-  constexpr int kKChunks = D / 8;                         // 16-byte chunks per K row
-  constexpr int kKItems = kBlockK * kKChunks / kThreads;  // K chunks per thread
-  constexpr int kVItems = (kBlockK / 4) * (D / 8);        // (4-key group, d-chunk) items
+  using St = PrefillStage<D>;
   constexpr int kDBlocks = D / 32;
   constexpr int kKSteps = D / 16;
 
-  __shared__ __align__(16) uint16_t lds[2 * L::stage];
+  __shared__ __align__(1024) uint16_t stage0[St::kElems];
+  __shared__ __align__(1024) uint16_t stage1[St::kElems];
 
   // ---- which (q tile, head, sequence): heaviest (last) q tiles first --------
   int qtile, head, seq;
@@ -124,9 +158,9 @@ void prefill_fwd_kernel(PrefillParams p) {
   const int rext = p.rel_extent;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lane = tid & 63;
-  const int col = lane & 31;   // query column of this lane
+  const int col = lane & 31;   // query column of this lane (per row block)
   const int half = lane >> 5;  // 0 / 1
 
   // ---- per-(sequence, head) buffer resources --------------------------------------
@@ -152,240 +186,317 @@ void prefill_fwd_kernel(PrefillParams p) {
   const int kt_end = kend > kbeg ? (kend + kBlockK - 1) / kBlockK : kt_beg;
 
   // ---- per-wave rows ---------------------------------------------------------
-  const int qa = q0 + 32 * wave;               // first row of the wave (local)
-  const int wrows = max(0, min(32, lq - qa));  // valid rows of the wave
-  const int qi = qa + col;                     // this lane's query (local)
-  const bool row_ok = qi < lq;
+  const int qa = q0 + 32 * kNqb * wave;                  // first row of the wave (local)
+  const int wrows = max(0, min(32 * kNqb, lq - qa));     // valid rows of the wave
   int wkend = lk, wkbeg = 0;
   if (!p.no_prune) {
     if (p.causal) wkend = min(lk, qa + wrows);
     if (wl >= 0) wkbeg = max(0, qa - wl);
   }
-
-  // ---- Q fragment (B operand), kept for the whole loop -----------------------
-  u32x4_t qf[kKSteps];
+  int qi[kNqb];        // this lane's query (local) in each row block
+  bool row_ok[kNqb];
 #pragma unroll
-  for (int kk = 0; kk < kKSteps; ++kk)
-    qf[kk] = buf_load_16(rq, (uint32_t)(qi * p.q_st + 16 * kk + 8 * half) * 2);
+  for (int qb = 0; qb < kNqb; ++qb) {
+    qi[qb] = qa + 32 * qb + col;
+    row_ok[qb] = qi[qb] < lq;
+  }
+
+  // ---- Q fragments (B operand), kept for the whole loop ----------------------
+  u32x4_t qf[kNqb][kKSteps];
+#pragma unroll
+  for (int qb = 0; qb < kNqb; ++qb)
+#pragma unroll
+    for (int kk = 0; kk < kKSteps; ++kk)
+      qf[qb][kk] = buf_load_16(rq, (uint32_t)(qi[qb] * p.q_st + 16 * kk + 8 * half) * 2);
 
   const float c2 = p.scale_log2;  // softmax_scale * log2(e)
-  float m_run = -INFINITY;         // running max (log2 domain), same in both halves
-  float l_run = 0.f;               // partial row sum over this half's keys
-  f32x16_t o[kDBlocks];
+  float m_run[kNqb];               // running max (log2 domain), same in both halves
+  float l_run[kNqb];               // partial row sum over this half's keys
+  f32x16_t o[kNqb][kDBlocks];
 #pragma unroll
-  for (int db = 0; db < kDBlocks; ++db) o[db] = f32x16_t{};
+  for (int qb = 0; qb < kNqb; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_run[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < kDBlocks; ++db) o[qb][db] = f32x16_t{};
+  }
 
-  // ---- K/V tile loader (global -> registers -> LDS) ---------------------------
-  u32x4_t kreg[kKItems];
-  u32x4_t vreg[4];
-  const bool v_loader = tid < kVItems;
-  const int v_kg = tid % (kBlockK / 4);  // 4-key group
-  const int v_dc = tid / (kBlockK / 4);  // 8-wide d chunk
-
-  auto load_tile = [&](int kt) {
+  // ---- K/V tile DMA: HBM -> LDS, rows past the sequence end read as zero -----------
+  // A wave DMA writes 64 x 16 contiguous bytes = kRowsPerDma rows; lane L fills
+  // slot L % kChunks of row L / kChunks with the chunk that swizzles to it.
+  const int dma_row = lane / St::kChunks;
+  const int dma_slot = lane % St::kChunks;
+  auto dma_tile = [&](int kt, uint16_t* stage) {
     const int kb = kt * kBlockK;
 #pragma unroll
-    for (int r = 0; r < kKItems; ++r) {
-      const int item = tid + r * kThreads;
-      const int row = item / kKChunks;
-      const int ch = item % kKChunks;
-      kreg[r] = buf_load_16(rk, (uint32_t)(kb + row) * k_row + 16 * ch);
-    }
-    if (v_loader) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        vreg[r] = buf_load_16(rv, (uint32_t)(kb + 4 * v_kg + r) * v_row + 16 * v_dc);
-    }
-  };
-  auto store_tile = [&](int buf) {
-    uint16_t* kl = lds + buf * L::stage;
-    uint16_t* vl = kl + L::kElems;
-#pragma unroll
-    for (int r = 0; r < kKItems; ++r) {
-      const int item = tid + r * kThreads;
-      const int row = item / kKChunks;
-      const int ch = item % kKChunks;
-      *reinterpret_cast<u32x4_t*>(kl + row * L::kPitch + 8 * ch) = kreg[r];
-    }
-    if (v_loader) {
-      // vreg[r] holds V[key 4*kg + r][d 8*dc .. 8*dc+7]; write V^T rows d with
-      // the 4 keys side by side (8 bytes) at the permuted key position.
-      const int pos = vt_pos(4 * v_kg);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t lo01 = __builtin_amdgcn_perm(vreg[1][w], vreg[0][w], 0x05040100u);
-        const uint32_t lo23 = __builtin_amdgcn_perm(vreg[3][w], vreg[2][w], 0x05040100u);
-        const uint32_t hi01 = __builtin_amdgcn_perm(vreg[1][w], vreg[0][w], 0x07060302u);
-        const uint32_t hi23 = __builtin_amdgcn_perm(vreg[3][w], vreg[2][w], 0x07060302u);
-        const int d0 = 8 * v_dc + 2 * w;
-        *reinterpret_cast<u32x2_t*>(vl + d0 * L::vPitch + pos) = u32x2_t{lo01, lo23};
-        *reinterpret_cast<u32x2_t*>(vl + (d0 + 1) * L::vPitch + pos) = u32x2_t{hi01, hi23};
-      }
+    for (int u = 0; u < St::kDmaPerWave; ++u) {
+      const int id = wave * St::kDmaPerWave + u;  // 0 .. 2*kDmaPerTensor-1
+      const bool is_v = id >= St::kDmaPerTensor;
+      const int blk = is_v ? id - St::kDmaPerTensor : id;
+      const int row = blk * St::kRowsPerDma + dma_row;
+      const int chunk = dma_slot ^ swz<St::kChunks>(row);
+      uint16_t* dst = stage + (is_v ? St::kTile : 0) + blk * 512;
+      const uint32_t off = (uint32_t)(kb + row) * (is_v ? v_row : k_row) + 16 * chunk;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_v ? rv : rk,
+                                               (__attribute__((address_space(3))) void*)dst, 16,
+                                               (int)off, 0, 0, 0);
     }
   };
 
-  // Bias resource: the (sequence, head) rows of the bias; this lane reads its row.
+  // Bias resource: the (sequence, head) rows of the bias; each lane reads its rows.
   const rsrc_t rrel = make_rsrc(
       static_cast<const char*>(p.rel) + ((int64_t)qs * p.rel_st + (int64_t)head * p.rel_sh) *
                                             Rel::kBytes,
       span_bytes(lq, p.rel_st, p.rel_width, Rel::kBytes));
-  const uint32_t rel_row_off = (uint32_t)(qi * p.rel_st) * Rel::kBytes;
 
-  if (kt_beg < kt_end) load_tile(kt_beg);
-  for (int kt = kt_beg; kt < kt_end; ++kt) {
-    const int buf = (kt - kt_beg) & 1;
-    store_tile(buf);
-    __syncthreads();
-    if (kt + 1 < kt_end) load_tile(kt + 1);
+  // Lane constants of the LDS fragment reads.
+  // K (A operand of QK): row 32*blk + col, chunk 2*kk + half.
+  // V^T (A operand of PV, two transposing reads): 16-lane group gq = lane / 16,
+  // lane i = lane % 16 of the group addresses V[k0 + i/4][d0 + 4*(i%4)] with
+  // d0 = 32*db + 16*(gq % 2) and k0 = 16*t + 4*half (+ 8 for the second read).
+  const int tr_i = lane & 15;
+  const int tr_row = tr_i >> 2;                         // + k0
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (tr_i & 3);  // + 32*db
 
+  auto compute = [&](int kt, const uint16_t* stage) {
     const int kb = kt * kBlockK;
     // Wave-uniform activity / class of this tile.
     const bool active = wrows > 0 && kb < wkend && kb + kBlockK > wkbeg;
-    if (!active) continue;
+    if (!active) return;
     const int imin = qa, imax = qa + wrows - 1;
     const int jmin = kb, jmax = kb + kBlockK - 1;
     const bool need_mask = jmax >= lk || (p.causal && jmax > imin) ||
                            (wl >= 0 && imax - jmin > wl);
     const bool has_bias =
         rext > 0 && (imax + delta - jmin >= 0) && (imin + delta - jmax <= rext - 1);
+    const uint16_t* kl = stage;
+    const uint16_t* vl = stage + St::kTile;
 
-    const uint16_t* kl = lds + buf * L::stage;
-    const uint16_t* vl = kl + L::kElems;
-
-    // ---- S^T = K Q^T -----------------------------------------------------------
-    f32x16_t s[kBlockK / 32];
+    // ---- S^T = K Q^T (each K fragment feeds every row block) ---------------------
+    f32x16_t s[kNqb][kBlockK / 32];
 #if IFA4_PRIO
     __builtin_amdgcn_s_setprio(1);
 #endif
 #pragma unroll
     for (int blk = 0; blk < kBlockK / 32; ++blk) {
-      s[blk] = f32x16_t{};
-      const uint16_t* krow = kl + (32 * blk + col) * L::kPitch + 8 * half;
+#pragma unroll
+      for (int qb = 0; qb < kNqb; ++qb) s[qb][blk] = f32x16_t{};
+      const int row = 32 * blk + col;
+      const uint16_t* krow = kl + row * D;
+      const int sw = swz<St::kChunks>(row);
 #pragma unroll
       for (int kk = 0; kk < kKSteps; ++kk) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(krow + 16 * kk);
-        s[blk] = E::mfma32(a, qf[kk], s[blk]);
+        const u32x4_t a =
+            *reinterpret_cast<const u32x4_t*>(krow + 8 * ((2 * kk + half) ^ sw));
+#pragma unroll
+        for (int qb = 0; qb < kNqb; ++qb) s[qb][blk] = E::mfma32(a, qf[qb][kk], s[qb][blk]);
       }
     }
-
+#if IFA4_SCHED
+    // Keep kLookK fragment reads in flight ahead of the MFMAs (the default
+    // schedule waits for each LDS read right before its MFMA).
+    {
+      constexpr int kReads = (kBlockK / 32) * kKSteps;
+      __builtin_amdgcn_sched_group_barrier(0x100, kLookK, 0);
+#pragma unroll
+      for (int i = 0; i < kReads - kLookK; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, kNqb, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kNqb * kLookK, 0);
+    }
+#endif
 #if IFA4_PRIO
     __builtin_amdgcn_s_setprio(0);
 #endif
+
     // ---- logits (log2 domain) and tile max ---------------------------------------
-    // Element (blk, e) of this lane is tile-local key 32*blk + 8*(e>>2) + (e&3)
+    // Element (blk, e) of a lane is tile-local key 32*blk + 8*(e>>2) + (e&3)
     // + 4*half; `kc` below drops the lane term, which is folded into the bounds.
     float sc;  // factor applied inside the exponent FMA
-    float mx = -INFINITY;
+    float mx[kNqb];
     if (need_mask || has_bias) {
       sc = 1.f;
-      int hi = lk - 1 - kb;
-      if (p.causal) hi = min(hi, qi - kb);
-      if (!row_ok) hi = -1;
-      const int lo = wl >= 0 ? qi - wl - kb : -1;
-      const int hi_h = hi - 4 * half, lo_h = lo - 4 * half;
-      const int dbase = qi + delta - kb - 4 * half;  // dist = dbase - kc
-      float bias[kBlockK / 2];
-      if (has_bias) {
 #pragma unroll
-        for (int blk = 0; blk < kBlockK / 32; ++blk)
+      for (int qb = 0; qb < kNqb; ++qb) {
+        int hi = lk - 1 - kb;
+        if (p.causal) hi = min(hi, qi[qb] - kb);
+        if (!row_ok[qb]) hi = -1;
+        const int lo = wl >= 0 ? qi[qb] - wl - kb : -1;
+        const int hi_h = hi - 4 * half, lo_h = lo - 4 * half;
+        const int dbase = qi[qb] + delta - kb - 4 * half;  // dist = dbase - kc
+        const uint32_t rel_row_off = (uint32_t)(qi[qb] * p.rel_st) * Rel::kBytes;
+        float m = -INFINITY;
+#pragma unroll
+        for (int blk = 0; blk < kBlockK / 32; ++blk) {
+          float bias[16];
+          if (has_bias) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
+              const int dist = dbase - kc;
+              const uint32_t off = (uint32_t)dist < (uint32_t)rext
+                                       ? rel_row_off + (uint32_t)dist * Rel::kBytes
+                                       : kOutOfRange;
+              bias[e] = Rel::load(rrel, off);
+            }
+          }
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
-            const int dist = dbase - kc;
-            const uint32_t off = (uint32_t)dist < (uint32_t)rext
-                                     ? rel_row_off + (uint32_t)dist * Rel::kBytes
-                                     : kOutOfRange;
-            bias[16 * blk + e] = Rel::load(rrel, off);
+            float x = s[qb][blk][e] * c2;
+            if (has_bias) x = fmaf(bias[e], kLog2e, x);
+            x = (kc >= lo_h && kc <= hi_h) ? x : -INFINITY;
+            s[qb][blk][e] = x;
+            m = fmaxf(m, x);
           }
-      }
-#pragma unroll
-      for (int blk = 0; blk < kBlockK / 32; ++blk) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
-          float x = s[blk][e] * c2;
-          if (has_bias) x = fmaf(bias[16 * blk + e], kLog2e, x);
-          x = (kc >= lo_h && kc <= hi_h) ? x : -INFINITY;
-          s[blk][e] = x;
-          mx = fmaxf(mx, x);
         }
+        mx[qb] = m;
       }
     } else {
       sc = c2;
 #pragma unroll
-      for (int blk = 0; blk < kBlockK / 32; ++blk)
+      for (int qb = 0; qb < kNqb; ++qb) {
+        float m = -INFINITY;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[blk][e]);
-      mx *= c2;
+        for (int blk = 0; blk < kBlockK / 32; ++blk)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) m = fmaxf(m, s[qb][blk][e]);
+        mx[qb] = m * c2;
+      }
     }
-    mx = max_xor32(mx);
 
     // ---- deferred rescale ----------------------------------------------------------
-    const float m_cand = fmaxf(m_run, mx);
-    const bool grow = m_cand > m_run + kRescaleThreshold;
-    if (wave_any(grow)) {
-      const float m_upd = grow ? m_cand : m_run;
-      const float alpha = grow ? fast_exp2(m_run - m_upd) : 1.f;
-      l_run *= alpha;
+    bool grow[kNqb];
+    bool any_grow = false;
 #pragma unroll
-      for (int db = 0; db < kDBlocks; ++db)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
-      m_run = m_upd;
+    for (int qb = 0; qb < kNqb; ++qb) {
+      mx[qb] = max_xor32(mx[qb]);
+      const float m_cand = fmaxf(m_run[qb], mx[qb]);
+      grow[qb] = m_cand > m_run[qb] + kRescaleThreshold;
+      mx[qb] = m_cand;
+      any_grow |= grow[qb];
     }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    if (wave_any(any_grow)) {
+#pragma unroll
+      for (int qb = 0; qb < kNqb; ++qb) {
+        const float m_upd = grow[qb] ? mx[qb] : m_run[qb];
+        const float alpha = grow[qb] ? fast_exp2(m_run[qb] - m_upd) : 1.f;
+        l_run[qb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < kDBlocks; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[qb][db][e] *= alpha;
+        m_run[qb] = m_upd;
+      }
+    }
 
     // ---- P = exp2(x - m), packed to the PV B operand, row sum ----------------------
-    u32x4_t pb[kBlockK / 16];
+    u32x4_t pb[kNqb][kBlockK / 16];
 #pragma unroll
-    for (int t = 0; t < kBlockK / 16; ++t) {
-      float pv[8];
+    for (int qb = 0; qb < kNqb; ++qb) {
+      const float m_use = m_run[qb] == -INFINITY ? 0.f : m_run[qb];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pv[e] = fast_exp2(fmaf(s[t >> 1][8 * (t & 1) + e], sc, -m_use));
-        l_run += pv[e];
+      for (int t = 0; t < kBlockK / 16; ++t) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pv[e] = fast_exp2(fmaf(s[qb][t >> 1][8 * (t & 1) + e], sc, -m_use));
+          l_run[qb] += pv[e];
+        }
+        pb[qb][t] = u32x4_t{E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]),
+                            E::pack2(pv[4], pv[5]), E::pack2(pv[6], pv[7])};
       }
-      pb[t] = u32x4_t{E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
-                      E::pack2(pv[6], pv[7])};
     }
 
-    // ---- O^T += V^T P^T ----------------------------------------------------------
+    // ---- O^T += V^T P^T (each V^T fragment feeds every row block) -------------------
 #if IFA4_PRIO
     __builtin_amdgcn_s_setprio(1);
 #endif
 #pragma unroll
     for (int db = 0; db < kDBlocks; ++db) {
-      const uint16_t* vrow = vl + (32 * db + col) * L::vPitch + 8 * half;
 #pragma unroll
       for (int t = 0; t < kBlockK / 16; ++t) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(vrow + 16 * t);
-        o[db] = E::mfma32(a, pb[t], o[db]);
+        u32x2_t part[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int row = 16 * t + 8 * r + 4 * half + tr_row;
+          const int c = 32 * db + tr_col;  // element column, multiple of 4
+          const uint16_t* src = vl + row * D + 8 * ((c >> 3) ^ swz<St::kChunks>(row)) + (c & 7);
+          part[r] = __builtin_bit_cast(
+              u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                           (__attribute__((address_space(3))) s16x4_t*)src));
+        }
+        const u32x4_t a = {part[0][0], part[0][1], part[1][0], part[1][1]};
+#pragma unroll
+        for (int qb = 0; qb < kNqb; ++qb) o[qb][db] = E::mfma32(a, pb[qb][t], o[qb][db]);
       }
     }
+#if IFA4_SCHED
+    // Same for the PV product: kLookV operand pairs (two transposing reads
+    // each) in flight ahead of the MFMAs.
+    {
+      constexpr int kGroups = kDBlocks * (kBlockK / 16);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * kLookV, 1);
+#pragma unroll
+      for (int i = 0; i < kGroups - kLookV; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, kNqb, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kNqb * kLookV, 1);
+    }
+#endif
 #if IFA4_PRIO
     __builtin_amdgcn_s_setprio(0);
 #endif
+  };
+
+  // ---- pipeline: DMA of tile kt+1 in flight while tile kt is computed -------------
+  // Per tile: issue the next DMA; wait until only that DMA is outstanding for
+  // this wave (its part of the current tile has landed); barrier (every wave's
+  // part has landed); compute; barrier (the stage may be overwritten next).
+  // The two stages are distinct LDS objects so the compiler tracks them apart.
+  auto step = [&](int kt, uint16_t* cur, uint16_t* nxt) {
+    if (kt + 1 < kt_end) {
+      dma_tile(kt + 1, nxt);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(St::kDmaPerWave));
+    } else {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    compute(kt, cur);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  if (kt_beg < kt_end) dma_tile(kt_beg, stage0);
+  for (int kt = kt_beg; kt < kt_end; kt += 2) {
+    step(kt, stage0, stage1);
+    if (kt + 1 < kt_end) step(kt + 1, stage1, stage0);
   }
 
   // ---- epilogue: normalise, store O and LSE ------------------------------------------
-  const float l_tot = add_xor32(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (row_ok) {
-    uint16_t* obase = static_cast<uint16_t*>(p.out) + (int64_t)(qs + qi) * p.o_st +
-                      (int64_t)head * p.o_sh;
 #pragma unroll
-    for (int db = 0; db < kDBlocks; ++db) {
+  for (int qb = 0; qb < kNqb; ++qb) {
+    const float l_tot = add_xor32(l_run[qb]);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (row_ok[qb]) {
+      uint16_t* obase = static_cast<uint16_t*>(p.out) + (int64_t)(qs + qi[qb]) * p.o_st +
+                        (int64_t)head * p.o_sh;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 32 * db + 8 * i + 4 * half;
-        const u32x2_t w = {E::pack2(o[db][4 * i] * inv, o[db][4 * i + 1] * inv),
-                           E::pack2(o[db][4 * i + 2] * inv, o[db][4 * i + 3] * inv)};
-        *reinterpret_cast<u32x2_t*>(obase + d) = w;
+      for (int db = 0; db < kDBlocks; ++db) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * db + 8 * i + 4 * half;
+          const u32x2_t w = {E::pack2(o[qb][db][4 * i] * inv, o[qb][db][4 * i + 1] * inv),
+                             E::pack2(o[qb][db][4 * i + 2] * inv, o[qb][db][4 * i + 3] * inv)};
+          *reinterpret_cast<u32x2_t*>(obase + d) = w;
+        }
       }
-    }
-    if (p.lse != nullptr && half == 0) {
-      const float lse = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
-      p.lse[(int64_t)head * p.lse_sh + qs + qi] = lse;
+      if (p.lse != nullptr && half == 0) {
+        const float lse = l_tot > 0.f ? (m_run[qb] + __log2f(l_tot)) * kLn2 : -INFINITY;
+        p.lse[(int64_t)head * p.lse_sh + qs + qi[qb]] = lse;
+      }
     }
   }
 }
