@@ -139,6 +139,22 @@ __device__ __forceinline__ uint32_t buf_load_2(rsrc_t r, uint32_t byte_off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)byte_off, 0, 0);
 }
 
+// Direct HBM -> LDS load of 16 bytes per lane: lane L's bytes land at
+// lds_dst + 16 L (lds_dst wave-uniform), out-of-range lanes write zeros.
+// Written as inline asm on purpose: the compiler's wait-count pass cannot tell
+// which LDS bytes a DMA writes, so with the builtin it puts a full vmcnt wait
+// in front of LDS reads of the *other* stage, draining the prefetch of the next
+// tile every iteration.  Hidden from the compiler, the DMA is ordered only by
+// the kernel's explicit s_waitcnt + s_barrier; the compiler's own waits for its
+// loads stay correct because loads complete in issue order (they only wait
+// longer when a DMA was issued after the load they wait for).
+__device__ __forceinline__ void dma_16(rsrc_t r, uint32_t byte_off, const void* lds_dst) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst);
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(r), "{m0}"(m0)
+               : "memory");
+}
+
 // Bias element types: storage size and conversion of the loaded bits to fp32.
 struct RelF32 {
   static constexpr int kBytes = 4;

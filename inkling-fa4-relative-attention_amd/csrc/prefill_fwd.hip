@@ -63,6 +63,9 @@
 #ifndef IFA4_SCHED
 #define IFA4_SCHED 1
 #endif
+#ifndef IFA4_PV2
+#define IFA4_PV2 1
+#endif
 
 namespace ifa4 {
 namespace {
@@ -120,8 +123,12 @@ void prefill_fwd_kernel(PrefillParams p) {
   constexpr int kDBlocks = D / 32;
   constexpr int kKSteps = D / 16;
 
-  __shared__ __align__(1024) uint16_t stage0[St::kElems];
-  __shared__ __align__(1024) uint16_t stage1[St::kElems];
+  // Both stages in one array: a read of stage 1 is the stage-0 address plus a
+  // constant, which folds into the instruction's offset (one address register
+  // per fragment instead of one per fragment and stage).
+  __shared__ __align__(1024) uint16_t stages[2 * St::kElems];
+  uint16_t* const stage0 = stages;
+  uint16_t* const stage1 = stages + St::kElems;
 
   // ---- which (q tile, head, sequence): heaviest (last) q tiles first --------
   int qtile, head, seq;
@@ -237,9 +244,7 @@ void prefill_fwd_kernel(PrefillParams p) {
       const int chunk = dma_slot ^ swz<St::kChunks>(row);
       uint16_t* dst = stage + (is_v ? St::kTile : 0) + blk * 512;
       const uint32_t off = (uint32_t)(kb + row) * (is_v ? v_row : k_row) + 16 * chunk;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(is_v ? rv : rk,
-                                               (__attribute__((address_space(3))) void*)dst, 16,
-                                               (int)off, 0, 0, 0);
+      dma_16(is_v ? rv : rk, off, dst);
     }
   };
 
@@ -308,6 +313,28 @@ void prefill_fwd_kernel(PrefillParams p) {
 #endif
 #if IFA4_PRIO
     __builtin_amdgcn_s_setprio(0);
+#endif
+
+#if IFA4_PV2
+    // V^T operand of key block t for d block db: two transposing reads.
+    auto read_vt = [&](int db, int t) -> u32x4_t {
+      u32x2_t part[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int row = 16 * t + 8 * r + 4 * half + tr_row;
+        const int c = 32 * db + tr_col;  // element column, multiple of 4
+        const uint16_t* src = vl + row * D + 8 * ((c >> 3) ^ swz<St::kChunks>(row)) + (c & 7);
+        part[r] = __builtin_bit_cast(
+            u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                         (__attribute__((address_space(3))) s16x4_t*)src));
+      }
+      return u32x4_t{part[0][0], part[0][1], part[1][0], part[1][1]};
+    };
+    // Key block 0's V^T fragments are read now; their latency hides behind the
+    // softmax below.
+    u32x4_t vfr[kDBlocks];
+#pragma unroll
+    for (int db = 0; db < kDBlocks; ++db) vfr[db] = read_vt(db, 0);
 #endif
 
     // ---- logits (log2 domain) and tile max ---------------------------------------
@@ -391,6 +418,68 @@ void prefill_fwd_kernel(PrefillParams p) {
       }
     }
 
+#if IFA4_PV2
+    // ---- P = exp2(x - m) per 16-key block t, then O^T += V^T P^T -------------------
+    // Key-block-major: the MFMAs of block t run while block t+1's exponentials
+    // are computed and its V^T fragments are read.
+    float m_use[kNqb];
+#pragma unroll
+    for (int qb = 0; qb < kNqb; ++qb) m_use[qb] = m_run[qb] == -INFINITY ? 0.f : m_run[qb];
+    auto make_p = [&](int qb, int t) -> u32x4_t {
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = fast_exp2(fmaf(s[qb][t >> 1][8 * (t & 1) + e], sc, -m_use[qb]));
+        l_run[qb] += pv[e];
+      }
+      return u32x4_t{E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
+                     E::pack2(pv[6], pv[7])};
+    };
+    u32x4_t pcur[kNqb];
+#pragma unroll
+    for (int qb = 0; qb < kNqb; ++qb) pcur[qb] = make_p(qb, 0);
+#if IFA4_PRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
+#pragma unroll
+    for (int t = 0; t < kBlockK / 16; ++t) {
+      u32x4_t pnext[kNqb];
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) {
+#pragma unroll
+        for (int qb = 0; qb < kNqb; ++qb) o[qb][db] = E::mfma32(vfr[db], pcur[qb], o[qb][db]);
+        if (t + 1 < kBlockK / 16) vfr[db] = read_vt(db, t + 1);
+      }
+      if (t + 1 < kBlockK / 16) {
+#pragma unroll
+        for (int qb = 0; qb < kNqb; ++qb) pnext[qb] = make_p(qb, t + 1);
+#pragma unroll
+        for (int qb = 0; qb < kNqb; ++qb) pcur[qb] = pnext[qb];
+      }
+    }
+#if IFA4_SCHED
+    // Per key block t < 3: each MFMA followed by the two reads of the next
+    // block's fragment and a share of the next block's exponentials.
+    {
+      constexpr int kT = kBlockK / 16;
+      constexpr int kPValu = 7;  // ~28 VALU/TRANS per block of P over 4 MFMAs
+#pragma unroll
+      for (int t = 0; t < kT - 1; ++t) {
+#pragma unroll
+        for (int db = 0; db < kDBlocks; ++db) {
+          __builtin_amdgcn_sched_group_barrier(0x008, kNqb, 1);
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+          __builtin_amdgcn_sched_group_barrier(0x402, kPValu * kNqb, 1);
+        }
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kNqb * kDBlocks, 1);
+    }
+#endif
+#if IFA4_PRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+  };
+#else
     // ---- P = exp2(x - m), packed to the PV B operand, row sum ----------------------
     u32x4_t pb[kNqb][kBlockK / 16];
 #pragma unroll
@@ -450,12 +539,14 @@ void prefill_fwd_kernel(PrefillParams p) {
     __builtin_amdgcn_s_setprio(0);
 #endif
   };
+#endif
 
   // ---- pipeline: DMA of tile kt+1 in flight while tile kt is computed -------------
   // Per tile: issue the next DMA; wait until only that DMA is outstanding for
   // this wave (its part of the current tile has landed); barrier (every wave's
   // part has landed); compute; barrier (the stage may be overwritten next).
-  // The two stages are distinct LDS objects so the compiler tracks them apart.
+  // The DMA is invisible to the compiler (dma_16), so these waits are the only
+  // ordering between a stage's DMA and its reads.
   auto step = [&](int kt, uint16_t* cur, uint16_t* nxt) {
     if (kt + 1 < kt_end) {
       dma_tile(kt + 1, nxt);
@@ -469,7 +560,9 @@ void prefill_fwd_kernel(PrefillParams p) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+  // First tile in flight together with the Q fragments; one wait for both.
   if (kt_beg < kt_end) dma_tile(kt_beg, stage0);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   for (int kt = kt_beg; kt < kt_end; kt += 2) {
     step(kt, stage0, stage1);
     if (kt + 1 < kt_end) step(kt + 1, stage1, stage0);
