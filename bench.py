@@ -57,13 +57,14 @@ def settle(fn, seconds=0.5):
         torch.cuda.synchronize()
 
 
-def time_gpu(fn, steps, warmup):
+def time_gpu(fn, steps, warmup, settle_s=0.5):
     """Average ms per call of `fn` over `steps` back-to-back calls, bracketed by
     HIP events on the current stream (where the operator launches).  The
-    clocks are settled first, then `warmup` untimed calls run."""
+    clocks are settled first (`settle_s` seconds), then `warmup` untimed calls
+    run."""
     import torch
 
-    settle(fn)
+    settle(fn, settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -153,7 +154,7 @@ def copy_bandwidth():
     n = 1 << 30
     a = torch.empty(n, dtype=torch.uint8, device="cuda")
     b = torch.empty_like(a)
-    ms = time_gpu(lambda: b.copy_(a), 10, 3)
+    ms = time_gpu(lambda: b.copy_(a), 10, 3, settle_s=0.05)
     return 2 * n / (ms * 1e-3) / 1e9
 
 
@@ -313,7 +314,8 @@ def main():
         log(f"decode: {args.steps} steps")
         dec = decode_bench(args.steps, args.warmup)
         log(f"decode: {dec['us']:.1f} us  {dec['gbps']:.0f} GB/s")
-        result["decode"] = {**dec, "roofline": {"bound": "hbm", "kernel": "decode_split_kernel",
+        result["decode"] = {**dec, "roofline": {"bound": "hbm",
+                                                "kernel": "decode_split_kernel + decode_combine_kernel",
                                                 "achieved": round(dec["gbps"], 1),
                                                 "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                                                 "frac": round(dec["frac_of_peak"], 4),
@@ -323,12 +325,13 @@ def main():
             result["unit"] = "GB/s"
             result["ms_per_step"] = round(dec["us"] / 1e3, 5)
             result["roofline"] = result["decode"]["roofline"]
-    try:
-        result["copy_gbps"] = round(copy_bandwidth(), 1)
-        log(f"device copy bandwidth: {result['copy_gbps']} GB/s")
-    except RuntimeError as e:  # out of memory on a busy device: report, continue
-        result["copy_gbps"] = None
-        log(f"copy bandwidth skipped: {e}")
+    if args.only == "all":
+        try:
+            result["copy_gbps"] = round(copy_bandwidth(), 1)
+            log(f"device copy bandwidth: {result['copy_gbps']} GB/s")
+        except RuntimeError as e:  # out of memory on a busy device: report, continue
+            result["copy_gbps"] = None
+            log(f"copy bandwidth skipped: {e}")
     if not args.skip_cpu and case is not None:
         log("cpu baseline (fp32 oracle, one sequence)")
         result["cpu_baseline"] = cpu_baseline(case)

@@ -4,7 +4,7 @@
 //
 // Prefill: one shape for every sequence length.  The kernel is written for
 // 4 waves x 32 query rows (BLOCK_Q 128) and 64-key KV tiles in two LDS stages
-// (71,680 B of LDS at head_dim 128, so two workgroups fit in the 160 KiB of a
+// (64 KiB of LDS at head_dim 128, so two workgroups fit in the 160 KiB of a
 // CU); the shape is a compile-time property of the kernel, listed here so the
 // host reports what runs.
 //
