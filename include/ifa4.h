@@ -102,7 +102,7 @@ typedef struct ifa4_tile {
   int32_t block_k;        /* keys per KV tile */
   int32_t waves;          /* wavefronts per workgroup */
   int32_t stages;         /* LDS buffers for K/V */
-  int32_t kv_chunk;       /* decode: keys per split (0 for prefill) */
+  int32_t kv_chunk;       /* decode: most keys one wave streams (0 for prefill) */
 } ifa4_tile;
 
 /* Human-readable name of a status code; never NULL. */
@@ -137,10 +137,15 @@ int32_t ifa4_prefill_count_tiles(const ifa4_args* args, const int32_t* host_cu_s
                                  int64_t* total);
 
 /*
- * Decode: exactly one query token per sequence (total_q == batch).  Split-KV:
- * pass 1 writes one (o, lse) partial per (sequence, head, KV split) into the
- * workspace, pass 2 merges the splits by log-sum-exp and writes out/lse.
- * Replaces inkling_fa4_rel_attention_decode_triton
+ * Decode: exactly one query token per sequence (total_q == batch).  Split-KV,
+ * stream-K: pass 1 runs min(2048, steps) persistent waves over all
+ * (sequence, kv head) caches laid end to end in 32-key steps, each wave an
+ * equal range; it writes one (o, lse) partial per (cache, wave) it touches
+ * into the workspace.  Pass 2 merges each cache's partials by log-sum-exp and
+ * writes out/lse.  The workspace (ifa4_decode_workspace_bytes, 256-byte
+ * aligned, contents on entry irrelevant) is scratch for one call; calls that
+ * share a workspace must not overlap.  Replaces
+ * inkling_fa4_rel_attention_decode_triton
  * (src/inkling_fa4/triton_kernel_decode.py:127-170).
  */
 size_t ifa4_decode_workspace_bytes(const ifa4_args* args);

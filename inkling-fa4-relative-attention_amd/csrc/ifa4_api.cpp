@@ -114,14 +114,25 @@ ifa4::PrefillParams make_prefill_params(const ifa4_args* a) {
   return p;
 }
 
-int64_t decode_splits(const ifa4_args* a, int32_t chunk) {
-  const int64_t keys = a->causal ? (a->max_seqlen_k > 0 ? 1 : 0) : a->max_seqlen_k;
-  const int64_t s = (keys + chunk - 1) / chunk;
-  return s < 1 ? 1 : s;
+int32_t decode_waves(const ifa4_args* a) {
+  return ifa4::decode_waves_for(a->batch, a->kv_heads, a->max_seqlen_k, a->causal != 0);
 }
 
-int32_t decode_chunk(const ifa4_args* a) {
-  return ifa4::decode_chunk_for(a->batch, a->kv_heads, a->max_seqlen_k);
+// Decode workspace: partial (o, lse) slots, one per (segment, wave) pair that
+// can exist (batch * kv_heads + waves), then the per-segment wave ranges.
+struct DecodeLayout {
+  int64_t slots, o_bytes, lse_bytes, meta_bytes;
+  int64_t total() const { return o_bytes + lse_bytes + meta_bytes; }
+};
+DecodeLayout decode_layout(const ifa4_args* a) {
+  DecodeLayout l;
+  const int64_t segs = (int64_t)a->batch * a->kv_heads;
+  const int64_t group = a->n_heads / a->kv_heads;
+  l.slots = segs + decode_waves(a);
+  l.o_bytes = (l.slots * group * a->head_dim * 4 + 255) / 256 * 256;
+  l.lse_bytes = (l.slots * group * 4 + 255) / 256 * 256;
+  l.meta_bytes = segs * 2 * 4;
+  return l;
 }
 
 int32_t check_decode(const ifa4_args* a) {
@@ -210,21 +221,23 @@ int32_t ifa4_prefill_count_tiles(const ifa4_args* args, const int32_t* cu_q, con
 
 size_t ifa4_decode_workspace_bytes(const ifa4_args* args) {
   if (check_decode(args) != IFA4_OK) return 0;
-  const int64_t splits = decode_splits(args, decode_chunk(args));
-  const int64_t rows = (int64_t)args->batch * args->n_heads * splits;
-  const int64_t o_bytes = ((rows * args->head_dim * 4) + 255) / 256 * 256;
-  return (size_t)(o_bytes + rows * 4);
+  return (size_t)decode_layout(args).total();
 }
 
 int32_t ifa4_decode_tile(const ifa4_args* args, ifa4_tile* tile) {
   if (tile == nullptr) return IFA4_EINVAL;
   const int32_t st = check_decode(args);
   if (st != IFA4_OK) return st;
+  // One wave per workgroup, 32-key steps, two register stages; kv_chunk = the
+  // most keys one persistent wave streams (ceil(steps / waves) steps).
   tile->block_q = 1;
-  tile->block_k = 64;
+  tile->block_k = ifa4::kDecodeStep;
   tile->waves = 1;
-  tile->stages = 1;
-  tile->kv_chunk = decode_chunk(args);
+  tile->stages = 2;
+  const int64_t steps = ifa4::decode_max_steps(args->batch, args->kv_heads, args->max_seqlen_k,
+                                               args->causal != 0);
+  const int32_t w = decode_waves(args);
+  tile->kv_chunk = w > 0 ? (int32_t)(((steps + w - 1) / w) * ifa4::kDecodeStep) : 0;
   return IFA4_OK;
 }
 
@@ -236,10 +249,7 @@ int32_t ifa4_decode_fwd(const ifa4_args* args, void* workspace, size_t workspace
   const size_t need = ifa4_decode_workspace_bytes(args);
   if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256))
     return IFA4_EWORKSPACE;
-  const int32_t chunk = decode_chunk(args);
-  const int64_t splits = decode_splits(args, chunk);
-  const int64_t rows = (int64_t)args->batch * args->n_heads * splits;
-  const int64_t o_bytes = ((rows * args->head_dim * 4) + 255) / 256 * 256;
+  const DecodeLayout lay = decode_layout(args);
 
   ifa4::DecodeParams p{};
   p.q = args->q;
@@ -251,7 +261,9 @@ int32_t ifa4_decode_fwd(const ifa4_args* args, void* workspace, size_t workspace
   p.cu_q = args->cu_seqlens_q;
   p.cu_k = args->cu_seqlens_k;
   p.ws_o = static_cast<float*>(workspace);
-  p.ws_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes);
+  p.ws_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + lay.o_bytes);
+  p.ws_meta = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + lay.o_bytes +
+                                         lay.lse_bytes);
   p.q_st = args->q_stride_t;
   p.q_sh = args->q_stride_h;
   p.k_st = args->k_stride_t;
@@ -270,8 +282,7 @@ int32_t ifa4_decode_fwd(const ifa4_args* args, void* workspace, size_t workspace
   p.rel_extent = args->rel_extent;
   p.causal = args->causal;
   p.rel_dtype = args->rel_dtype;
-  p.chunk = chunk;
-  p.n_splits = (int32_t)splits;
+  p.n_waves = decode_waves(args);
   p.scale_log2 = args->softmax_scale * kLog2eHost;
   const hipError_t e = ifa4::launch_decode(p, args->head_dim, args->qkv_dtype,
                                            static_cast<hipStream_t>(stream));

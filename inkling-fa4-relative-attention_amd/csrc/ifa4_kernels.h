@@ -40,8 +40,9 @@ struct DecodeParams {
   float* lse;
   const int32_t* cu_q;
   const int32_t* cu_k;
-  float* ws_o;    // [batch, n_heads, n_splits, head_dim]
-  float* ws_lse;  // [batch, n_heads, n_splits] (log2 domain)
+  float* ws_o;        // [batch * kv_heads + n_waves][group][head_dim] partials
+  float* ws_lse;      // [batch * kv_heads + n_waves][group] (log2 domain)
+  int32_t* ws_meta;   // [batch * kv_heads][2]: first and last wave of a segment
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, rel_st, rel_sh, o_st, o_sh, lse_sh;
   int32_t batch;
   int32_t n_heads;
@@ -50,8 +51,7 @@ struct DecodeParams {
   int32_t rel_extent;
   int32_t causal;
   int32_t rel_dtype;
-  int32_t chunk;     // keys per split (multiple of 64)
-  int32_t n_splits;  // ceil(max_seqlen_k / chunk)
+  int32_t n_waves;   // persistent waves of pass 1 (0: nothing to stream)
   float scale_log2;
 };
 

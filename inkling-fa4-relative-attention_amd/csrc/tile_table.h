@@ -8,9 +8,9 @@
 // CU); the shape is a compile-time property of the kernel, listed here so the
 // host reports what runs.
 //
-// Decode: keys per KV split.  The split count is ceil(max_seqlen_k / chunk);
-// the chunk is the largest power-of-two multiple of 64 that still gives at
-// least kDecodeTargetWaves split waves, so short caches are split finer.
+// Decode: persistent waves of the stream-K pass.  The decode kernel runs two
+// waves per SIMD, so 2048 waves are one resident round on the 256 CUs of an
+// MI355X; the grid never exceeds the number of 32-key steps a call can have.
 #pragma once
 
 #include <stdint.h>
@@ -30,18 +30,24 @@ constexpr PrefillTileEntry kPrefillTiles[] = {
     {128, 128, 64, 4, 2},
 };
 
-#ifndef IFA4_DECODE_TARGET_WAVES
-#define IFA4_DECODE_TARGET_WAVES 8192
+#ifndef IFA4_DECODE_WAVES
+#define IFA4_DECODE_WAVES 2048
 #endif
-constexpr int32_t kDecodeChunks[] = {1024, 512, 256, 128, 64};
-constexpr int64_t kDecodeTargetWaves = IFA4_DECODE_TARGET_WAVES;
+constexpr int64_t kDecodeWaves = IFA4_DECODE_WAVES;
+constexpr int32_t kDecodeStep = 32;  // keys per step of a decode wave
 
-inline int32_t decode_chunk_for(int64_t batch, int64_t kv_heads, int64_t max_seqlen_k) {
-  for (int32_t c : kDecodeChunks) {
-    const int64_t splits = (max_seqlen_k + c - 1) / c;
-    if (batch * kv_heads * splits >= kDecodeTargetWaves) return c;
-  }
-  return kDecodeChunks[sizeof(kDecodeChunks) / sizeof(kDecodeChunks[0]) - 1];
+// Upper bound of the 32-key steps of a decode call: every (sequence, kv head)
+// at max_seqlen_k keys (one key when causal: top-left alignment, Lq = 1).
+inline int64_t decode_max_steps(int64_t batch, int64_t kv_heads, int64_t max_seqlen_k,
+                                bool causal) {
+  const int64_t keys = causal ? (max_seqlen_k > 0 ? 1 : 0) : max_seqlen_k;
+  return batch * kv_heads * ((keys + kDecodeStep - 1) / kDecodeStep);
+}
+
+inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seqlen_k,
+                                bool causal) {
+  const int64_t t = decode_max_steps(batch, kv_heads, max_seqlen_k, causal);
+  return (int32_t)(t < kDecodeWaves ? t : kDecodeWaves);
 }
 
 }  // namespace ifa4

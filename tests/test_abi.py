@@ -123,8 +123,13 @@ def test_decode_workspace_and_contract():
     assert lib.ifa4_decode_workspace_bytes(ctypes.byref(a_causal)) < ws
     tile = _abi.Ifa4Tile()
     assert lib.ifa4_decode_tile(ctypes.byref(a), ctypes.byref(tile)) == _abi.IFA4_OK
-    splits = -(-16384 // tile.kv_chunk)
-    assert ws >= 64 * 8 * splits * (128 + 1) * 4
+    # stream-K: min(2048, steps) persistent waves; one (o, lse) partial slot per
+    # (segment, wave) pair that can occur = segments + waves; then 2 ints per segment
+    segs, group = 64 * 2, 8 // 2
+    steps = segs * (16384 // 32)
+    waves = min(2048, steps)
+    assert tile.kv_chunk == 32 * -(-steps // waves)
+    assert ws >= (segs + waves) * group * (128 + 1) * 4 + segs * 2 * 4
     # missing / small workspace is reported, nothing launched
     assert lib.ifa4_decode_fwd(ctypes.byref(a), None, 0, None) == _abi.IFA4_EWORKSPACE
     assert lib.ifa4_decode_fwd(ctypes.byref(a), 256, ws - 1, None) == _abi.IFA4_EWORKSPACE
