@@ -33,8 +33,8 @@
 // records the range of waves that cover the segment.
 //
 // Pass 2 (decode_combine_kernel): per (head, sequence) merge of the segment's
-// partials by log-sum-exp (four waves share them, wave-parallel max/sum);
-// writes out (q dtype) and lse (natural log).
+// partials by log-sum-exp (four waves share them, each merging online); writes
+// out (q dtype) and lse (natural log).
 #include "ifa4_device.hpp"
 #include "ifa4_kernels.h"
 
@@ -427,91 +427,98 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
   }
 }
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
-  return x;
-}
-
 constexpr int kCombineWaves = 4;
 
-// One workgroup per (head, sequence); wave v merges parts v, v+4, ... of the
-// head's segment with independent loads in flight, the four partial sums meet
-// in LDS.
+// One workgroup per (head, sequence).  Two dependent memory rounds: the
+// sequence bounds and the segment's wave range (independent loads), then the
+// parts themselves.  Wave v merges parts v, v+4, ... online (running max,
+// rescaled sums, loads of later parts in flight); the four wave results meet in
+// LDS.
 template <int D, typename Tag>
 __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(DecodeParams p) {
   using E = Elem<Tag>;
   constexpr int kPer = D / 64;  // d values per lane
-  __shared__ float part[kCombineWaves - 1][64 * kPer];
+  __shared__ float part_o[kCombineWaves][64 * kPer];
+  __shared__ float part_m[kCombineWaves];
+  __shared__ float part_l[kCombineWaves];
   const int head = blockIdx.x;
   const int seq = blockIdx.y;
-  const int qs = p.cu_q[seq];
-  const int lq = p.cu_q[seq + 1] - qs;
-  const int lk = p.cu_k[seq + 1] - p.cu_k[seq];
-  if (lq != 1) return;
-  const int kend = p.causal ? min(lk, 1) : lk;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int ga = p.group;
   const int kvh = head / ga, h = head % ga;
   const int seg = seq * p.kv_heads + kvh;
+  const int qs = p.cu_q[seq];
+  const int lq = p.cu_q[seq + 1] - qs;
+  const int lk = p.cu_k[seq + 1] - p.cu_k[seq];
+  const int meta_first = p.ws_meta[2 * seg];  // read before knowing it is needed
+  const int meta_last = p.ws_meta[2 * seg + 1];
+  if (lq != 1) return;
+  const int kend = p.causal ? min(lk, 1) : lk;
   int w_first = 0, parts = 0;
   if (seq_steps(lq, kend) > 0 && p.n_waves > 0) {
     // clamped so that a slot index can never leave the workspace
-    w_first = min(max(p.ws_meta[2 * seg], 0), p.n_waves - 1);
-    const int w_last = min(max(p.ws_meta[2 * seg + 1], w_first), p.n_waves - 1);
-    parts = w_last - w_first + 1;
+    w_first = min(max(meta_first, 0), p.n_waves - 1);
+    parts = min(max(meta_last, w_first), p.n_waves - 1) - w_first + 1;
   }
   // part i of the segment lives in slot seg + w_first + i
   const float* lse_s = p.ws_lse + (int64_t)(seg + w_first) * ga + h;
   const float* o_s = p.ws_o + ((int64_t)(seg + w_first) * ga + h) * D + kPer * lane;
   const int64_t o_stride = (int64_t)ga * D;
 
-  // Every wave computes the max and the weight sum over all parts.
-  float m = -INFINITY;
-  for (int s = lane; s < parts; s += 64) m = fmaxf(m, lse_s[(int64_t)s * ga]);
-  m = wave_max(m);
-  const float m_use = m == -INFINITY ? 0.f : m;
-  float wpart = 0.f;
-  for (int s = lane; s < parts; s += 64) wpart += fast_exp2(lse_s[(int64_t)s * ga] - m_use);
-  const float wsum = wave_sum(wpart);
-
+  float m = -INFINITY, l = 0.f;
   float acc[kPer];
 #pragma unroll
   for (int e = 0; e < kPer; ++e) acc[e] = 0.f;
-#pragma unroll 8
+#pragma unroll 4
   for (int s = wave; s < parts; s += kCombineWaves) {
-    const float wu = fast_exp2(lse_s[(int64_t)s * ga] - m_use);
+    const float ls = lse_s[(int64_t)s * ga];
+    float os[kPer];
 #pragma unroll
-    for (int e = 0; e < kPer; ++e) acc[e] = fmaf(wu, o_s[s * o_stride + e], acc[e]);
+    for (int e = 0; e < kPer; ++e) os[e] = o_s[s * o_stride + e];
+    const float mn = fmaxf(m, ls);
+    const float mu = mn == -INFINITY ? 0.f : mn;
+    const float a_old = fast_exp2(m - mu), a_new = fast_exp2(ls - mu);
+    l = l * a_old + a_new;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) acc[e] = acc[e] * a_old + a_new * os[e];
+    m = mn;
   }
-  if (wave > 0) {
 #pragma unroll
-    for (int e = 0; e < kPer; ++e) part[wave - 1][kPer * lane + e] = acc[e];
+  for (int e = 0; e < kPer; ++e) part_o[wave][kPer * lane + e] = acc[e];
+  if (lane == 0) {
+    part_m[wave] = m;
+    part_l[wave] = l;
   }
   __syncthreads();
   if (wave != 0) return;
+  float mt = part_m[0];
 #pragma unroll
-  for (int v = 0; v < kCombineWaves - 1; ++v)
+  for (int v = 1; v < kCombineWaves; ++v) mt = fmaxf(mt, part_m[v]);
+  const float mu = mt == -INFINITY ? 0.f : mt;
+  float lt = 0.f;
+  float out[kPer];
 #pragma unroll
-    for (int e = 0; e < kPer; ++e) acc[e] += part[v][kPer * lane + e];
+  for (int e = 0; e < kPer; ++e) out[e] = 0.f;
+#pragma unroll
+  for (int v = 0; v < kCombineWaves; ++v) {
+    const float a = fast_exp2(part_m[v] - mu);
+    lt += a * part_l[v];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) out[e] += a * part_o[v][kPer * lane + e];
+  }
 
-  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
   uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)qs * p.o_st + (int64_t)head * p.o_sh +
                   kPer * lane;
   if constexpr (kPer == 2) {
-    *reinterpret_cast<uint32_t*>(dst) = E::pack2(acc[0] * inv, acc[1] * inv);
+    *reinterpret_cast<uint32_t*>(dst) = E::pack2(out[0] * inv, out[1] * inv);
   } else {
-    const uint32_t wv = E::pack2(acc[0] * inv, 0.f);
+    const uint32_t wv = E::pack2(out[0] * inv, 0.f);
     *dst = (uint16_t)(wv & 0xffffu);
   }
   if (p.lse != nullptr && lane == 0) {
-    p.lse[(int64_t)head * p.lse_sh + qs] = wsum > 0.f ? (m_use + __log2f(wsum)) * kLn2 : -INFINITY;
+    p.lse[(int64_t)head * p.lse_sh + qs] = lt > 0.f ? (mu + __log2f(lt)) * kLn2 : -INFINITY;
   }
 }
 
