@@ -60,6 +60,9 @@
 #ifndef IFA4_PREFILL_NQB
 #define IFA4_PREFILL_NQB 1
 #endif
+#ifndef IFA4_BIAS_LDS
+#define IFA4_BIAS_LDS 1
+#endif
 #ifndef IFA4_SCHED
 #define IFA4_SCHED 1
 #endif
@@ -105,9 +108,18 @@ __device__ __forceinline__ int swz(int row) {
   return (((row & 3) << 2) | ((row >> 2) & 3)) & (kChunks - 1);
 }
 
-// s_waitcnt immediate: wait until at most n vector-memory operations of this
-// wave are outstanding (LDS/export counters left unconstrained).
+// s_waitcnt immediates: at most n vector-memory operations of this wave
+// outstanding (LDS/export counters unconstrained); all LDS operations done.
 constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+constexpr int kLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
+
+// Bias table in LDS, for the layout where every token of the sequence shares
+// one per-head table (token stride 0): log2(e) * rel[dist] at index
+// kBiasPad + dist, zeros for dist outside [0, rel_extent).  A tile that has
+// bias sees dist in an interval of 32 + 64 - 1 values that meets
+// [0, rel_extent), so the padding covers every read: no range checks.
+constexpr int kBiasPad = 96;
+constexpr int kBiasLdsMax = 1024;  // longest table staged in LDS
 
 // Bytes a resource over `rows` rows of `stride` elements (row length d) spans.
 __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int d, int esize) {
@@ -127,6 +139,7 @@ void prefill_fwd_kernel(PrefillParams p) {
   // constant, which folds into the instruction's offset (one address register
   // per fragment instead of one per fragment and stage).
   __shared__ __align__(1024) uint16_t stages[2 * St::kElems];
+  __shared__ float bias_lds[2 * kBiasPad + kBiasLdsMax];
   uint16_t* const stage0 = stages;
   uint16_t* const stage1 = stages + St::kElems;
 
@@ -253,6 +266,8 @@ void prefill_fwd_kernel(PrefillParams p) {
       static_cast<const char*>(p.rel) + ((int64_t)qs * p.rel_st + (int64_t)head * p.rel_sh) *
                                             Rel::kBytes,
       span_bytes(lq, p.rel_st, p.rel_width, Rel::kBytes));
+  // Shared-table layout with a table short enough to stage in LDS.
+  const bool bias_in_lds = IFA4_BIAS_LDS && p.rel_st == 0 && rext > 0 && rext <= kBiasLdsMax;
 
   // Lane constants of the LDS fragment reads.
   // K (A operand of QK): row 32*blk + col, chunk 2*kk + half.
@@ -356,8 +371,16 @@ void prefill_fwd_kernel(PrefillParams p) {
         float m = -INFINITY;
 #pragma unroll
         for (int blk = 0; blk < kBlockK / 32; ++blk) {
-          float bias[16];
-          if (has_bias) {
+          float bias[16];  // log2(e) * bias
+          if (has_bias && bias_in_lds) {
+            // element e at dist = dbase - kc: a constant offset from one base
+            const float* tb = bias_lds + kBiasPad + dbase - (kBlockK - 1);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
+              bias[e] = tb[kBlockK - 1 - kc];
+            }
+          } else if (has_bias) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
               const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
@@ -365,15 +388,15 @@ void prefill_fwd_kernel(PrefillParams p) {
               const uint32_t off = (uint32_t)dist < (uint32_t)rext
                                        ? rel_row_off + (uint32_t)dist * Rel::kBytes
                                        : kOutOfRange;
-              bias[e] = Rel::load(rrel, off);
+              bias[e] = Rel::load(rrel, off) * kLog2e;
             }
           }
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
             float x = s[qb][blk][e] * c2;
-            if (has_bias) x = fmaf(bias[e], kLog2e, x);
-            x = (kc >= lo_h && kc <= hi_h) ? x : -INFINITY;
+            if (has_bias) x += bias[e];
+            if (need_mask) x = (kc >= lo_h && kc <= hi_h) ? x : -INFINITY;
             s[qb][blk][e] = x;
             m = fmaxf(m, x);
           }
@@ -560,9 +583,31 @@ void prefill_fwd_kernel(PrefillParams p) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  // First tile in flight together with the Q fragments; one wait for both.
+  // The bias table (shared-table layout) is read with the Q fragments and the
+  // first tile; one wait for all three, then it goes to LDS.  The first tile's
+  // barrier publishes it.
+  constexpr int kBiasPer = (2 * kBiasPad + kBiasLdsMax + kThreads - 1) / kThreads;
+  float tab[kBiasPer];
+  if (bias_in_lds) {
+#pragma unroll
+    for (int i = 0; i < kBiasPer; ++i) {
+      const int idx = tid + i * kThreads;  // table index + kBiasPad
+      const int dist = idx - kBiasPad;
+      const uint32_t off = (uint32_t)dist < (uint32_t)rext ? (uint32_t)dist * Rel::kBytes
+                                                            : kOutOfRange;
+      tab[i] = Rel::load(rrel, off) * kLog2e;
+    }
+  }
   if (kt_beg < kt_end) dma_tile(kt_beg, stage0);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if (bias_in_lds) {
+#pragma unroll
+    for (int i = 0; i < kBiasPer; ++i) {
+      const int idx = tid + i * kThreads;
+      if (idx < 2 * kBiasPad + kBiasLdsMax) bias_lds[idx] = tab[i];
+    }
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+  }
   for (int kt = kt_beg; kt < kt_end; kt += 2) {
     step(kt, stage0, stage1);
     if (kt + 1 < kt_end) step(kt + 1, stage1, stage0);

@@ -95,3 +95,44 @@ def test_decode_empty_kv_rows(cuda):
     want = _oracle(case)
     torch.testing.assert_close(out[1].float(), want[0][1].float(), atol=ATOL, rtol=RTOL)
     torch.testing.assert_close(lse[:, 1], want[1][:, 1], atol=LSE_ATOL, rtol=0)
+
+
+# ---- stream-K partition: every cache laid end to end in 32-key steps, split
+# evenly over min(2048, steps) persistent waves ---------------------------------------
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_decode_stream_many_short_caches(cuda, causal):
+    """150 sequences (three 64-sequence chunks of the device-side scan), empty and
+    one-key caches mixed in: waves cross many cache boundaries, the cursor reloads
+    sequence chunks, and empty caches own no steps."""
+    g = torch.Generator().manual_seed(11)
+    lens = torch.randint(0, 100, (150,), generator=g).tolist()
+    lens[3] = 0
+    lens[70] = 1
+    lens[140] = 32
+    case = testing.make_case("dec_short", [1] * 150, lens, 8, 2, 128, torch.bfloat16, seed=12,
+                             causal=causal)
+    out, lse = _decode(case, cuda)
+    want = _oracle(case)
+    live = torch.tensor([n > 0 for n in lens])
+    torch.testing.assert_close(out[live].float(), want[0][live].float(), atol=ATOL, rtol=RTOL)
+    torch.testing.assert_close(lse[:, live], want[1][:, live], atol=LSE_ATOL, rtol=0)
+    assert (out[~live].float() == 0).all() and torch.isneginf(lse[:, ~live]).all()
+
+
+def test_decode_stream_one_cache_over_all_waves(cuda):
+    """One 70,000-key cache per kv head: 2,188 steps each, 2,048 waves, so every
+    wave holds a piece and the merge of a head sums ~1,000 partials."""
+    case = testing.make_case("dec_long", [1], [70000], 8, 2, 128, torch.bfloat16, seed=13,
+                             causal=False)
+    _check(_decode(case, cuda), _oracle(case))
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_decode_stream_step_boundaries(cuda, head_dim):
+    """Cache lengths at and around multiples of the 32-key step, with more steps
+    than waves so wave ranges start and stop inside caches."""
+    lens = [31, 32, 33, 63, 64, 65, 95, 96, 97, 4096, 4097, 4127, 4128, 4129] * 5
+    case = testing.make_case("dec_steps", [1] * len(lens), lens, 4, 4, head_dim, torch.bfloat16,
+                             seed=14, causal=False)
+    _check(_decode(case, cuda), _oracle(case))
