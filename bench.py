@@ -315,11 +315,11 @@ def main():
         dec = decode_bench(args.steps, args.warmup)
         log(f"decode: {dec['us']:.1f} us  {dec['gbps']:.0f} GB/s")
         result["decode"] = {**dec, "roofline": {"bound": "hbm",
-                                                "kernel": "decode_split_kernel + decode_combine_kernel",
+                                                "kernel": "decode_stream_kernel + decode_combine_kernel",
                                                 "achieved": round(dec["gbps"], 1),
                                                 "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                                                 "frac": round(dec["frac_of_peak"], 4),
-                                                "traffic": traffic("decode_split_kernel")}}
+                                                "traffic": traffic("decode_stream_kernel")}}
         if result["value"] is None:
             result["value"] = round(dec["gbps"], 1)
             result["unit"] = "GB/s"
