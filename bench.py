@@ -8,9 +8,10 @@ with the reference's own 2*S^2*D*Hq*B count alongside.
 
 Also measured in the same run: split-KV decode (batch 64, one query per
 sequence, KV lengths U[1024,16384] seeded, non-causal so the whole cache is
-streamed) as KV GB/s against the 8 TB/s HBM peak; the other prefill sequence
-lengths {1024, 2048, 8192}; and the fp32 CPU oracle on a bounded sample as the
-CPU baseline.
+streamed) as KV GB/s against the 8 TB/s HBM peak, also with the same keys in
+a paged cache (blocks of 16 tokens, shuffled); the other prefill sequence
+lengths {1024, 2048, 8192}; and, as the CPU baseline, the fp32 CPU oracle over
+the whole headline batch (median of up to 3 passes, at most ~30 s).
 
 Usage:  python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
         [--only prefill|decode|all] [--seq 4096]
@@ -124,9 +125,12 @@ def prefill_bench(seq_len, steps, warmup, batch=8):
     }, case
 
 
-def decode_bench(steps, warmup):
+def decode_bench(steps, warmup, block_size=0):
+    """Decode over the 64-sequence batch; block_size > 0: the same keys in a
+    paged cache of that block size (blocks in a shuffled physical order)."""
     import torch
-    from inkling_fa4 import inkling_fa4_rel_attention_decode, testing
+    from inkling_fa4 import (inkling_fa4_rel_attention_decode,
+                             inkling_fa4_rel_attention_decode_paged, testing)
 
     case = testing.decode(causal=False)
     lens_k = (case.cu_k[1:] - case.cu_k[:-1])
@@ -135,16 +139,30 @@ def decode_bench(steps, warmup):
     esize = case.k.element_size()
     kv_bytes = sum_l * hkv * d * 2 * esize
     qo_bytes = 2 * case.q.numel() * esize
+    table_bytes = 0
     c = case.to("cuda")
     args = c.args()
+    if block_size:
+        pk = testing.paginate(case, block_size=block_size, seed=0, spare_blocks=0,
+                              fill=0.0).to("cuda")
+        table_bytes = 4 * int(((lens_k + block_size - 1) // block_size).sum())
 
-    def step():
-        return inkling_fa4_rel_attention_decode(*args, causal=False, softmax_scale=c.scale)
+        def step():
+            return inkling_fa4_rel_attention_decode_paged(
+                c.q, pk.k_cache, pk.v_cache, c.rel, c.cu_q, pk.seqused_k, pk.block_table,
+                c.max_q, c.max_k, c.rel_extent, causal=False, softmax_scale=c.scale)
+    else:
+        def step():
+            return inkling_fa4_rel_attention_decode(*args, causal=False, softmax_scale=c.scale)
 
     ms = time_gpu(step, steps, warmup)
-    gbps = (kv_bytes + qo_bytes) / (ms * 1e-3) / 1e9
-    return {"batch": case.q.shape[0], "sum_kv_len": sum_l, "bytes": kv_bytes + qo_bytes,
-            "us": ms * 1e3, "gbps": gbps, "frac_of_peak": gbps / HBM_PEAK_GBPS}
+    nbytes = kv_bytes + qo_bytes + table_bytes
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    out = {"batch": case.q.shape[0], "sum_kv_len": sum_l, "bytes": nbytes,
+           "us": ms * 1e3, "gbps": gbps, "frac_of_peak": gbps / HBM_PEAK_GBPS}
+    if block_size:
+        out["block_size"] = block_size
+    return out
 
 
 def copy_bandwidth():
@@ -158,9 +176,26 @@ def copy_bandwidth():
     return 2 * n / (ms * 1e-3) / 1e9
 
 
-def cpu_baseline(case, budget_s=10.0):
-    """fp32 CPU oracle on whole sequences of the headline batch (all heads),
-    one after another until `budget_s` seconds have elapsed or the batch is done."""
+def physical_cores():
+    """Distinct (package, core) pairs in /proc/cpuinfo; None where it is unreadable."""
+    try:
+        pairs, phys = set(), None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key == "physical id":
+                    phys = val.strip()
+                elif key == "core id":
+                    pairs.add((phys, val.strip()))
+        return len(pairs) or None
+    except OSError:
+        return None
+
+
+def cpu_baseline(case, repeats=3, budget_s=30.0):
+    """fp32 CPU oracle over the headline batch (every sequence, all heads),
+    timed `repeats` times (fewer if the budget is spent); the median is reported."""
     import torch
     from oracle import ref_rel_attn
 
@@ -170,26 +205,29 @@ def cpu_baseline(case, budget_s=10.0):
         threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     cq, ck = case.cu_q.tolist(), case.cu_k.tolist()
-    flops, done, t0 = 0.0, 0, time.perf_counter()
-    for b in range(len(cq) - 1):
-        q = case.q[cq[b]:cq[b + 1]]
-        k = case.k[ck[b]:ck[b + 1]]
-        v = case.v[ck[b]:ck[b + 1]]
-        rel = case.rel[cq[b]:cq[b + 1]]
-        lq = cq[b + 1] - cq[b]
-        cu = torch.tensor([0, lq], dtype=torch.int32)
-        ref_rel_attn(q, k, v, rel, cu, cu, case.scale, case.rel_extent, causal=True)
-        flops += 4.0 * q.shape[2] * (lq * (lq + 1) // 2) * q.shape[1]
-        done += 1
-        log(f"cpu baseline: sequence {b} done ({time.perf_counter() - t0:.1f} s)")
-        if time.perf_counter() - t0 >= budget_s:
+    flops = sum(4.0 * case.q.shape[2] * ((cq[b + 1] - cq[b]) * (cq[b + 1] - cq[b] + 1) // 2)
+                * case.q.shape[1] for b in range(len(cq) - 1))
+    times, t_start = [], time.perf_counter()
+    for r in range(repeats):
+        t0 = time.perf_counter()
+        for b in range(len(cq) - 1):
+            lq = cq[b + 1] - cq[b]
+            cu = torch.tensor([0, lq], dtype=torch.int32)
+            ref_rel_attn(case.q[cq[b]:cq[b + 1]], case.k[ck[b]:ck[b + 1]],
+                         case.v[ck[b]:ck[b + 1]], case.rel[cq[b]:cq[b + 1]], cu, cu,
+                         case.scale, case.rel_extent, causal=True)
+        times.append(time.perf_counter() - t0)
+        log(f"cpu baseline: pass {r} over the batch {times[-1]:.2f} s")
+        if time.perf_counter() - t_start + times[-1] > budget_s:
             break
-    dt = time.perf_counter() - t0
+    dt = sorted(times)[len(times) // 2]
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port", "seconds": round(dt, 2),
-            "sample": f"{done} of {len(cq) - 1} sequences of the headline batch "
-                      f"({cq[1] - cq[0]} tokens, all {case.q.shape[1]} heads each), "
-                      "fp32 oracle (dense per sequence/head) on the host CPU"}
+            "kind": "port", "seconds": round(dt, 6), "passes_s": [round(t, 6) for t in times],
+            "cpu_count": os.cpu_count(), "physical_cores": physical_cores(),
+            "sample": f"median of {len(times)} passes over the whole headline batch "
+                      f"({len(cq) - 1} sequences of {cq[1] - cq[0]} tokens, all "
+                      f"{case.q.shape[1]} heads), fp32 oracle (dense scores per sequence "
+                      "and head) on the host CPU"}
 
 
 def traffic(kernel):
@@ -320,6 +358,11 @@ def main():
                                                 "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                                                 "frac": round(dec["frac_of_peak"], 4),
                                                 "traffic": traffic("decode_stream_kernel")}}
+        log(f"decode, paged cache (block 16): {args.steps} steps")
+        dp = decode_bench(args.steps, args.warmup, block_size=16)
+        log(f"decode paged: {dp['us']:.1f} us  {dp['gbps']:.0f} GB/s")
+        result["decode_paged"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                  for k, v in dp.items()}
         if result["value"] is None:
             result["value"] = round(dec["gbps"], 1)
             result["unit"] = "GB/s"
@@ -333,7 +376,7 @@ def main():
             result["copy_gbps"] = None
             log(f"copy bandwidth skipped: {e}")
     if not args.skip_cpu and case is not None:
-        log("cpu baseline (fp32 oracle, one sequence)")
+        log("cpu baseline (fp32 oracle over the batch)")
         result["cpu_baseline"] = cpu_baseline(case)
         log(f"cpu baseline: {result['cpu_baseline']['value']:.4f} TFLOP/s "
             f"in {result['cpu_baseline']['seconds']:.1f} s")

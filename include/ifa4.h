@@ -153,6 +153,45 @@ int32_t ifa4_decode_tile(const ifa4_args* args, ifa4_tile* tile);
 int32_t ifa4_decode_fwd(const ifa4_args* args, void* workspace, size_t workspace_bytes,
                         void* stream);
 
+/*
+ * Paged KV cache, the serving caller's format (the reference's serving backend
+ * keeps KV in blocks of 16 tokens, outputs/architecture.md:117-120; the
+ * reference kernels themselves take contiguous varlen K/V only).  The cache is
+ * a pool of fixed-size blocks
+ *   k_cache, v_cache [num_blocks, block_size, kv_heads, head_dim]  (qkv_dtype)
+ * addressed as  base + blk * k_stride_block + row * args.k_stride_t
+ *                    + kv_head * args.k_stride_h  (elements; same for v).
+ * Sequence b holds seqused_k[b] keys; its key j sits in block
+ *   block_table[b * block_table_stride + j / block_size]  at row j % block_size.
+ * With a paged cache, args.k / args.v are the pool bases, args.cu_seqlens_k is
+ * not read (may be NULL), args.total_k is ignored, and args.max_seqlen_k must
+ * bound every seqused_k[b].  Keys are read only below seqused_k[b] (clamped to
+ * [0, max_blocks_per_seq * block_size]); a table entry outside [0, num_blocks)
+ * reads as zero keys and values instead of leaving the pool.
+ */
+typedef struct ifa4_paged_kv {
+  uint32_t struct_size;         /* sizeof(ifa4_paged_kv) */
+  int32_t block_size;           /* tokens per block: a power of two, 8 .. 65536 */
+  const int32_t* block_table;   /* device int32 [batch, block_table_stride] */
+  const int32_t* seqused_k;     /* device int32 [batch]: keys held by each sequence */
+  int64_t block_table_stride;   /* elements between the table rows of two sequences */
+  int64_t k_stride_block;       /* elements between two blocks of k_cache */
+  int64_t v_stride_block;       /* elements between two blocks of v_cache */
+  int32_t num_blocks;           /* blocks in the pool */
+  int32_t max_blocks_per_seq;   /* table entries per sequence, >= ceil(max_seqlen_k / block_size) */
+} ifa4_paged_kv;
+
+/*
+ * Decode over a paged KV cache: the same two passes as ifa4_decode_fwd with
+ * the same workspace layout, results bit-identical to ifa4_decode_fwd on the
+ * same keys stored contiguously.  Replaces the KV-cache read of the serving
+ * backend's flash_attn_varlen_func call (block_table / seqused_k arguments),
+ * outputs/architecture.md:117-120.
+ */
+size_t ifa4_decode_paged_workspace_bytes(const ifa4_args* args, const ifa4_paged_kv* kv);
+int32_t ifa4_decode_paged_fwd(const ifa4_args* args, const ifa4_paged_kv* kv, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -45,18 +45,22 @@ def _run(cmd):
         print(out)
 
 
-def build_library(jobs):
-    os.makedirs(BUILD, exist_ok=True)
+def build_library(jobs, out_dir=PKG, defines=(), build_dir=BUILD):
+    """Compile the kernels and the C ABI into out_dir/libifa4.so.  `defines`:
+    extra -D flags (tile-sweep knobs of the kernel sources)."""
+    os.makedirs(build_dir, exist_ok=True)
+    flags = HIP_FLAGS + [f"-D{d}" for d in defines]
     objs = []
     cmds = []
     for src in LIB_SOURCES:
-        obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+        obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        cmds.append([HIPCC] + HIP_FLAGS + lang + ["-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC] + flags + lang + ["-c", os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
-    out = os.path.join(PKG, LIB_NAME)
+    os.makedirs(out_dir, exist_ok=True)
+    out = os.path.join(out_dir, LIB_NAME)
     tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs)
     os.replace(tmp, out)

@@ -86,6 +86,14 @@ struct SeqChunk {
   int steps, excl, qs, ks, kend, lk;  // this lane's sequence
 };
 
+// Keys of sequence `seq` in a paged cache: seqused_k clamped to what the
+// table row can address.
+__device__ __forceinline__ int paged_len(const DecodeParams& p, int seq) {
+  const int cap = p.max_blocks << p.block_shift;
+  return min(max(p.seqused_k[seq], 0), cap);
+}
+
+template <bool kPaged>
 __device__ __forceinline__ SeqChunk load_chunk(const DecodeParams& p, int base, int excl0,
                                                int lane) {
   SeqChunk c;
@@ -96,8 +104,12 @@ __device__ __forceinline__ SeqChunk load_chunk(const DecodeParams& p, int base, 
   if (seq < p.batch) {
     c.qs = p.cu_q[seq];
     const int lq = p.cu_q[seq + 1] - c.qs;
-    c.ks = p.cu_k[seq];
-    c.lk = p.cu_k[seq + 1] - c.ks;
+    if constexpr (kPaged) {
+      c.lk = paged_len(p, seq);
+    } else {
+      c.ks = p.cu_k[seq];
+      c.lk = p.cu_k[seq + 1] - c.ks;
+    }
     c.kend = p.causal ? min(c.lk, 1) : c.lk;
     c.steps = seq_steps(lq, c.kend);
   }
@@ -117,7 +129,7 @@ struct Cursor {
   bool first;                 // first step of the segment in this wave
 };
 
-template <int D, typename Tag, int G>
+template <int D, typename Tag, int G, bool kPaged>
 __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
   using E = Elem<Tag>;
   using S = DecodeShape<D>;
@@ -138,16 +150,16 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
   const int g_act = p.group;
 
   // ---- total steps T (every wave derives the same), this wave's range ----------
-  SeqChunk ch = load_chunk(p, 0, 0, lane);
+  SeqChunk ch = load_chunk<kPaged>(p, 0, 0, lane);
   int total = ch.total_incl;
-  for (int b = 64; b < p.batch; b += 64) total = load_chunk(p, b, total, lane).total_incl;
+  for (int b = 64; b < p.batch; b += 64) total = load_chunk<kPaged>(p, b, total, lane).total_incl;
   const int T = hkv * total;
   if (T == 0) return;
   const int P = (T + W - 1) / W;
   const int g0 = w * P;
   const int g1 = min(g0 + P, T);
   if (g0 >= g1) return;
-  if (p.batch > 64) ch = load_chunk(p, 0, 0, lane);
+  if (p.batch > 64) ch = load_chunk<kPaged>(p, 0, 0, lane);
 
   // Cursor of global step gs (gs only moves forward; the chunk follows it).
   // Returns steps == 0 if gs lies past the last sequence (cannot happen for
@@ -180,27 +192,72 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
         none.steps = 0;
         return none;
       }
-      ch = load_chunk(p, ch.base + 64, ch.total_incl, lane);
+      ch = load_chunk<kPaged>(p, ch.base + 64, ch.total_incl, lane);
     }
   };
 
   // ---- loads of one step, Q of a segment ---------------------------------------------
   const uint32_t k_row = (uint32_t)p.k_st * 2, v_row = (uint32_t)p.v_st * 2;
-  auto load = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu) {
-    const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (int64_t)cu.ks * p.k_st +
-                            (int64_t)cu.kvh * p.k_sh;
-    const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (int64_t)cu.ks * p.v_st +
-                            (int64_t)cu.kvh * p.v_sh;
-    const rsrc_t rk =
-        make_rsrc_uniform(kbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.k_st + D) * 2));
-    const rsrc_t rv =
-        make_rsrc_uniform(vbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.v_st + D) * 2));
+  // Paged cache: lane L holds table entry tw_base + L of sequence tw_seq (a
+  // window of 64 blocks; a 32-key step never straddles two windows).  A step
+  // reads its 8-key row groups through one buffer resource per block, so rows
+  // past the sequence end and entries outside the pool read as zero.
+  int tw = -1, tw_seq = -1, tw_base = 0;
+  const int bmask = (1 << p.block_shift) - 1;
+  auto load_paged = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu) {
     const int k0 = cu.step * kStep;
+    const int blk0 = k0 >> p.block_shift;
+    if (cu.seq != tw_seq || blk0 < tw_base || blk0 >= tw_base + 64) {
+      tw_seq = cu.seq;
+      tw_base = blk0 & ~63;
+      const int nblk = (cu.lk + bmask) >> p.block_shift;
+      const int e = tw_base + lane;
+      tw = e < nblk ? p.block_table[(int64_t)cu.seq * p.bt_stride + e] : -1;
+    }
+    const uint32_t k_bytes = (uint32_t)(((int64_t)bmask * p.k_st + D) * 2);
+    const uint32_t v_bytes = (uint32_t)(((int64_t)bmask * p.v_st + D) * 2);
+    constexpr int kGroups = kStep / 8;
+    rsrc_t rk[kGroups], rv[kGroups];
+#pragma unroll
+    for (int grp = 0; grp < kGroups; ++grp) {
+      const int ent = __builtin_amdgcn_readlane(tw, ((k0 + 8 * grp) >> p.block_shift) - tw_base);
+      const bool ok = (unsigned)ent < (unsigned)p.num_blocks;
+      const int64_t eb = ok ? (int64_t)ent : 0;
+      rk[grp] = make_rsrc_uniform(static_cast<const uint16_t*>(p.k) + eb * p.k_sblk +
+                                      (int64_t)cu.kvh * p.k_sh,
+                                  ok ? k_bytes : 0u);
+      rv[grp] = make_rsrc_uniform(static_cast<const uint16_t*>(p.v) + eb * p.v_sblk +
+                                      (int64_t)cu.kvh * p.v_sh,
+                                  ok ? v_bytes : 0u);
+    }
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
-      const uint32_t row = (uint32_t)(k0 + S::kRpi * i + r);
-      kr[i] = buf_load_16(rk, row * k_row + 16 * c);
-      vr[i] = buf_load_16(rv, row * v_row + 16 * c);
+      const int key = k0 + S::kRpi * i + r;
+      const uint32_t row = (uint32_t)(key & bmask);
+      const bool valid = key < cu.kend;
+      kr[i] = buf_load_16(rk[(S::kRpi * i) / 8], valid ? row * k_row + 16 * c : kOutOfRange);
+      vr[i] = buf_load_16(rv[(S::kRpi * i) / 8], valid ? row * v_row + 16 * c : kOutOfRange);
+    }
+  };
+  auto load = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu) {
+    if constexpr (kPaged) {
+      load_paged(kr, vr, cu);
+    } else {
+      const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (int64_t)cu.ks * p.k_st +
+                              (int64_t)cu.kvh * p.k_sh;
+      const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (int64_t)cu.ks * p.v_st +
+                              (int64_t)cu.kvh * p.v_sh;
+      const rsrc_t rk =
+          make_rsrc_uniform(kbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.k_st + D) * 2));
+      const rsrc_t rv =
+          make_rsrc_uniform(vbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.v_st + D) * 2));
+      const int k0 = cu.step * kStep;
+#pragma unroll
+      for (int i = 0; i < S::kLoads; ++i) {
+        const uint32_t row = (uint32_t)(k0 + S::kRpi * i + r);
+        kr[i] = buf_load_16(rk, row * k_row + 16 * c);
+        vr[i] = buf_load_16(rv, row * v_row + 16 * c);
+      }
     }
   };
   // Q rows of the segment's heads -> q_lds[slot] as [head][D]; heads past the
@@ -450,7 +507,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
   const int seg = seq * p.kv_heads + kvh;
   const int qs = p.cu_q[seq];
   const int lq = p.cu_q[seq + 1] - qs;
-  const int lk = p.cu_k[seq + 1] - p.cu_k[seq];
+  const int lk = p.block_table != nullptr ? paged_len(p, seq) : p.cu_k[seq + 1] - p.cu_k[seq];
   const int meta_first = p.ws_meta[2 * seg];  // read before knowing it is needed
   const int meta_last = p.ws_meta[2 * seg + 1];
   if (lq != 1) return;
@@ -525,8 +582,12 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
 template <int D, typename Tag, int G>
 hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   if (p.n_waves > 0) {
-    hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G>), dim3(p.n_waves), dim3(64), 0, stream,
-                       p);
+    if (p.block_table != nullptr)
+      hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true>), dim3(p.n_waves), dim3(64), 0,
+                         stream, p);
+    else
+      hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false>), dim3(p.n_waves), dim3(64), 0,
+                         stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

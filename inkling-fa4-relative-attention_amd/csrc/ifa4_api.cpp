@@ -21,7 +21,9 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-int32_t check_args(const ifa4_args* a) {
+// kv != nullptr: K/V are a paged cache described by *kv (checked by
+// check_paged); cu_seqlens_k is then not read and may be NULL.
+int32_t check_args(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr) {
   if (a == nullptr) return IFA4_EINVAL;
   if (a->struct_size != sizeof(ifa4_args)) return IFA4_EINVAL;
   if (a->batch < 0 || a->n_heads < 1 || a->kv_heads < 1) return IFA4_EINVAL;
@@ -41,7 +43,7 @@ int32_t check_args(const ifa4_args* a) {
   if (!(std::isfinite(a->softmax_scale))) return IFA4_EINVAL;
   if (a->batch == 0) return IFA4_OK;  // nothing to read or write
   if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->out == nullptr ||
-      a->cu_seqlens_q == nullptr || a->cu_seqlens_k == nullptr)
+      a->cu_seqlens_q == nullptr || (kv == nullptr && a->cu_seqlens_k == nullptr))
     return IFA4_EINVAL;
   if (a->rel_extent > 0 && a->rel == nullptr) return IFA4_EINVAL;
   if (a->lse != nullptr) {
@@ -70,10 +72,36 @@ int32_t check_args(const ifa4_args* a) {
   const int64_t rel_esize = a->rel_dtype == IFA4_FP32 ? 4 : 2;
   const int64_t kLimit = int64_t(1) << 31;
   const int64_t kpad = 128;  // rows a tile may read past the end
+  // a paged cache is addressed one block at a time (check_paged)
+  const int64_t k_rows = kv == nullptr ? a->max_seqlen_k + kpad : 0;
   if ((a->max_seqlen_q + kpad) * a->q_stride_t * 2 >= kLimit ||
-      (a->max_seqlen_k + kpad) * a->k_stride_t * 2 >= kLimit ||
-      (a->max_seqlen_k + kpad) * a->v_stride_t * 2 >= kLimit ||
+      k_rows * a->k_stride_t * 2 >= kLimit || k_rows * a->v_stride_t * 2 >= kLimit ||
       ((a->max_seqlen_q + kpad) * a->rel_stride_t + a->rel_width) * rel_esize >= kLimit)
+    return IFA4_EUNSUPPORTED;
+  return IFA4_OK;
+}
+
+// Paged KV cache description (include/ifa4.h, ifa4_paged_kv).
+int32_t check_paged(const ifa4_args* a, const ifa4_paged_kv* kv) {
+  if (kv == nullptr || kv->struct_size != sizeof(ifa4_paged_kv)) return IFA4_EINVAL;
+  const int32_t bs = kv->block_size;
+  if (bs < 8 || bs > 65536 || (bs & (bs - 1)) != 0) return IFA4_EINVAL;
+  if (kv->block_table_stride < 0 || kv->k_stride_block < 0 || kv->v_stride_block < 0 ||
+      kv->num_blocks < 0 || kv->max_blocks_per_seq < 0)
+    return IFA4_EINVAL;
+  if (a->batch == 0) return IFA4_OK;
+  if (kv->block_table == nullptr || kv->seqused_k == nullptr || !aligned(kv->block_table, 4) ||
+      !aligned(kv->seqused_k, 4))
+    return IFA4_EINVAL;
+  if (kv->num_blocks < 1 || kv->max_blocks_per_seq < 1) return IFA4_EINVAL;
+  // the table row must address max_seqlen_k keys; key indices stay in int32
+  if ((int64_t)kv->max_blocks_per_seq * bs < a->max_seqlen_k) return IFA4_EINVAL;
+  if ((int64_t)kv->max_blocks_per_seq * bs > (int64_t(1) << 30)) return IFA4_EUNSUPPORTED;
+  // 16-byte loads from every block; one block of one kv head spans < 2 GiB
+  if ((kv->k_stride_block | kv->v_stride_block) % 8 != 0) return IFA4_EUNSUPPORTED;
+  const int64_t kLimit = int64_t(1) << 31;
+  if (((int64_t)(bs - 1) * a->k_stride_t + a->head_dim) * 2 >= kLimit ||
+      ((int64_t)(bs - 1) * a->v_stride_t + a->head_dim) * 2 >= kLimit)
     return IFA4_EUNSUPPORTED;
   return IFA4_OK;
 }
@@ -135,12 +163,70 @@ DecodeLayout decode_layout(const ifa4_args* a) {
   return l;
 }
 
-int32_t check_decode(const ifa4_args* a) {
-  const int32_t st = check_args(a);
+int32_t check_decode(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr) {
+  int32_t st = check_args(a, kv);
   if (st != IFA4_OK) return st;
+  if (kv != nullptr && (st = check_paged(a, kv)) != IFA4_OK) return st;
   if (a->batch > 0 && a->total_q != a->batch) return IFA4_EINVAL;  // one query per sequence
   if (a->n_heads / a->kv_heads > ifa4::decode_max_group()) return IFA4_EUNSUPPORTED;
   return IFA4_OK;
+}
+
+int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  const int32_t st = check_decode(args, kv);
+  if (st != IFA4_OK) return st;
+  if (args->batch == 0) return IFA4_OK;
+  const DecodeLayout lay = decode_layout(args);
+  if (workspace == nullptr || workspace_bytes < (size_t)lay.total() || !aligned(workspace, 256))
+    return IFA4_EWORKSPACE;
+
+  ifa4::DecodeParams p{};
+  p.q = args->q;
+  p.k = args->k;
+  p.v = args->v;
+  p.rel = args->rel;
+  p.out = args->out;
+  p.lse = args->lse;
+  p.cu_q = args->cu_seqlens_q;
+  p.cu_k = kv == nullptr ? args->cu_seqlens_k : nullptr;
+  p.ws_o = static_cast<float*>(workspace);
+  p.ws_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + lay.o_bytes);
+  p.ws_meta = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + lay.o_bytes +
+                                         lay.lse_bytes);
+  p.q_st = args->q_stride_t;
+  p.q_sh = args->q_stride_h;
+  p.k_st = args->k_stride_t;
+  p.k_sh = args->k_stride_h;
+  p.v_st = args->v_stride_t;
+  p.v_sh = args->v_stride_h;
+  p.rel_st = args->rel_stride_t;
+  p.rel_sh = args->rel_stride_h;
+  p.o_st = args->out_stride_t;
+  p.o_sh = args->out_stride_h;
+  p.lse_sh = args->lse_stride_h;
+  p.batch = args->batch;
+  p.n_heads = args->n_heads;
+  p.kv_heads = args->kv_heads;
+  p.group = args->n_heads / args->kv_heads;
+  p.rel_extent = args->rel_extent;
+  p.causal = args->causal;
+  p.rel_dtype = args->rel_dtype;
+  p.n_waves = decode_waves(args);
+  p.scale_log2 = args->softmax_scale * kLog2eHost;
+  if (kv != nullptr) {
+    p.block_table = kv->block_table;
+    p.seqused_k = kv->seqused_k;
+    p.bt_stride = kv->block_table_stride;
+    p.k_sblk = kv->k_stride_block;
+    p.v_sblk = kv->v_stride_block;
+    p.block_shift = __builtin_ctz((unsigned)kv->block_size);
+    p.num_blocks = kv->num_blocks;
+    p.max_blocks = kv->max_blocks_per_seq;
+  }
+  const hipError_t e = ifa4::launch_decode(p, args->head_dim, args->qkv_dtype,
+                                           static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IFA4_OK : IFA4_ELAUNCH;
 }
 
 }  // namespace
@@ -243,50 +329,18 @@ int32_t ifa4_decode_tile(const ifa4_args* args, ifa4_tile* tile) {
 
 int32_t ifa4_decode_fwd(const ifa4_args* args, void* workspace, size_t workspace_bytes,
                         void* stream) {
-  const int32_t st = check_decode(args);
-  if (st != IFA4_OK) return st;
-  if (args->batch == 0) return IFA4_OK;
-  const size_t need = ifa4_decode_workspace_bytes(args);
-  if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 256))
-    return IFA4_EWORKSPACE;
-  const DecodeLayout lay = decode_layout(args);
+  return run_decode(args, nullptr, workspace, workspace_bytes, stream);
+}
 
-  ifa4::DecodeParams p{};
-  p.q = args->q;
-  p.k = args->k;
-  p.v = args->v;
-  p.rel = args->rel;
-  p.out = args->out;
-  p.lse = args->lse;
-  p.cu_q = args->cu_seqlens_q;
-  p.cu_k = args->cu_seqlens_k;
-  p.ws_o = static_cast<float*>(workspace);
-  p.ws_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + lay.o_bytes);
-  p.ws_meta = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + lay.o_bytes +
-                                         lay.lse_bytes);
-  p.q_st = args->q_stride_t;
-  p.q_sh = args->q_stride_h;
-  p.k_st = args->k_stride_t;
-  p.k_sh = args->k_stride_h;
-  p.v_st = args->v_stride_t;
-  p.v_sh = args->v_stride_h;
-  p.rel_st = args->rel_stride_t;
-  p.rel_sh = args->rel_stride_h;
-  p.o_st = args->out_stride_t;
-  p.o_sh = args->out_stride_h;
-  p.lse_sh = args->lse_stride_h;
-  p.batch = args->batch;
-  p.n_heads = args->n_heads;
-  p.kv_heads = args->kv_heads;
-  p.group = args->n_heads / args->kv_heads;
-  p.rel_extent = args->rel_extent;
-  p.causal = args->causal;
-  p.rel_dtype = args->rel_dtype;
-  p.n_waves = decode_waves(args);
-  p.scale_log2 = args->softmax_scale * kLog2eHost;
-  const hipError_t e = ifa4::launch_decode(p, args->head_dim, args->qkv_dtype,
-                                           static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? IFA4_OK : IFA4_ELAUNCH;
+size_t ifa4_decode_paged_workspace_bytes(const ifa4_args* args, const ifa4_paged_kv* kv) {
+  if (check_decode(args, kv) != IFA4_OK) return 0;
+  return (size_t)decode_layout(args).total();
+}
+
+int32_t ifa4_decode_paged_fwd(const ifa4_args* args, const ifa4_paged_kv* kv, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (kv == nullptr) return IFA4_EINVAL;
+  return run_decode(args, kv, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -183,10 +183,17 @@ __device__ __forceinline__ uint32_t buf_load_2(rsrc_t r, uint32_t byte_off) {
 // the kernel's explicit s_waitcnt + s_barrier; the compiler's own waits for its
 // loads stay correct because loads complete in issue order (they only wait
 // longer when a DMA was issued after the load they wait for).
+// The compiler does not resolve hazards into inline asm either: a VALU write
+// of an SGPR (v_readfirstlane, or v_readlane restoring a spilled resource)
+// needs 5 wait states before a VMEM instruction reads that SGPR, and an SALU
+// write of M0 needs 1 before an LDS DMA reads it.  Without them the DMA reads
+// a stale resource (seen as wrong rows when the decode kernel spilled its Q
+// resource), so the asm starts with s_nop 4 (5 wait states).
 __device__ __forceinline__ void dma_16(rsrc_t r, uint32_t byte_off, const void* lds_dst) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_dst);
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(r), "{m0}"(m0)
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(byte_off), "s"(r),
+               "{m0}"(m0)
                : "memory");
 }
 

@@ -53,6 +53,15 @@ struct DecodeParams {
   int32_t rel_dtype;
   int32_t n_waves;   // persistent waves of pass 1 (0: nothing to stream)
   float scale_log2;
+  // Paged KV cache (block_table != nullptr): k/v are block pools, key j of
+  // sequence b is row j & (2^block_shift - 1) of block
+  // block_table[b * bt_stride + (j >> block_shift)]; lengths from seqused_k.
+  const int32_t* block_table;
+  const int32_t* seqused_k;
+  int64_t bt_stride, k_sblk, v_sblk;
+  int32_t block_shift;
+  int32_t num_blocks;
+  int32_t max_blocks;  // table entries per sequence
 };
 
 int prefill_block_q();

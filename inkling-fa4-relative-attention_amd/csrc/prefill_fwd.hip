@@ -85,7 +85,7 @@ constexpr int kWavesPerSimd = kNqb == 1 ? 2 : 1;
 #ifndef IFA4_LOOK_V
 #define IFA4_LOOK_V 4
 #endif
-constexpr int kLookK = IFA4_LOOK_K;  // K fragment reads in flight ahead of the QK MFMAs
+[[maybe_unused]] constexpr int kLookK = IFA4_LOOK_K;  // K fragment reads in flight ahead of the QK MFMAs
 [[maybe_unused]] constexpr int kLookV = IFA4_LOOK_V;  // V^T operand pairs in flight ahead of the PV MFMAs (PV2 off)
 
 // One LDS stage: K tile then V tile, each [kBlockK][D] row-major, swizzled.

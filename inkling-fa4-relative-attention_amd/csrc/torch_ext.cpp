@@ -1,6 +1,6 @@
 // Thin PyTorch-ROCm binding over the C ABI (include/ifa4.h).
 //
-// Registers torch.ops.inkling_fa4.fwd / .decode.  The binding checks tensor
+// Registers torch.ops.inkling_fa4.fwd / .decode / .decode_paged.  The binding checks tensor
 // devices, dtypes and shapes, allocates out / lse / the decode workspace from
 // torch's caching allocator, fills an ifa4_args and calls the library on the
 // current HIP stream.  No math happens here, and there is no fallback: a
@@ -156,6 +156,72 @@ std::tuple<at::Tensor, at::Tensor> decode(const at::Tensor& q, const at::Tensor&
   return {out, lse};
 }
 
+// Decode over a paged KV cache: k_cache / v_cache [num_blocks, block_size,
+// kv_heads, head_dim], block_table int32 [batch, max_blocks_per_seq],
+// seqused_k int32 [batch].  Same outputs as decode().
+std::tuple<at::Tensor, at::Tensor> decode_paged(
+    const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
+    const at::Tensor& rel, const at::Tensor& cu_q, const at::Tensor& seqused_k,
+    const at::Tensor& block_table, int64_t max_q, int64_t max_k, int64_t rel_extent, bool causal,
+    int64_t window_left, double softmax_scale, bool return_lse) {
+  TORCH_CHECK(k_cache.dim() == 4 && v_cache.dim() == 4,
+              "inkling_fa4.decode_paged: k_cache / v_cache must be "
+              "[num_blocks, block_size, kv_heads, head_dim]");
+  TORCH_CHECK(k_cache.sizes() == v_cache.sizes(),
+              "inkling_fa4.decode_paged: k_cache and v_cache shapes differ");
+  TORCH_CHECK(block_table.is_cuda() && seqused_k.is_cuda() &&
+                  block_table.device() == q.device() && seqused_k.device() == q.device(),
+              "inkling_fa4.decode_paged: block_table / seqused_k must be on q's GPU");
+  TORCH_CHECK(block_table.scalar_type() == at::kInt && seqused_k.scalar_type() == at::kInt,
+              "inkling_fa4.decode_paged: block_table and seqused_k must be int32");
+  TORCH_CHECK(block_table.dim() == 2 && block_table.stride(1) == 1,
+              "inkling_fa4.decode_paged: block_table must be 2-D with contiguous rows");
+  TORCH_CHECK(seqused_k.dim() == 1 && seqused_k.is_contiguous(),
+              "inkling_fa4.decode_paged: seqused_k must be 1-D contiguous");
+  TORCH_CHECK(block_table.size(0) == cu_q.numel() - 1 && seqused_k.numel() == cu_q.numel() - 1,
+              "inkling_fa4.decode_paged: block_table / seqused_k need one row per sequence");
+  // The per-token view [blocks * block_size, kv_heads, head_dim] of the first
+  // block carries the row / head strides; block strides travel separately.
+  const at::Tensor k_rows = k_cache.select(0, 0);
+  const at::Tensor v_rows = v_cache.select(0, 0);
+  ifa4_args a = make_args(q, k_rows, v_rows, rel, cu_q, cu_q, max_q, max_k, rel_extent, causal,
+                          window_left, softmax_scale, 0);
+  a.k = k_cache.data_ptr();
+  a.v = v_cache.data_ptr();
+  a.cu_seqlens_k = nullptr;
+  a.total_k = 0;
+  ifa4_paged_kv kv{};
+  kv.struct_size = sizeof(ifa4_paged_kv);
+  kv.block_size = static_cast<int32_t>(k_cache.size(1));
+  kv.block_table = block_table.data_ptr<int32_t>();
+  kv.seqused_k = seqused_k.data_ptr<int32_t>();
+  kv.block_table_stride = block_table.stride(0);
+  kv.k_stride_block = k_cache.stride(0);
+  kv.v_stride_block = v_cache.stride(0);
+  kv.num_blocks = static_cast<int32_t>(k_cache.size(0));
+  kv.max_blocks_per_seq = static_cast<int32_t>(block_table.size(1));
+
+  at::Tensor out = at::empty_like(q, q.options().memory_format(at::MemoryFormat::Contiguous));
+  at::Tensor lse = return_lse ? at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat))
+                              : at::empty({0}, q.options().dtype(at::kFloat));
+  a.out = out.data_ptr();
+  a.out_stride_t = out.stride(0);
+  a.out_stride_h = out.stride(1);
+  if (return_lse) {
+    a.lse = lse.data_ptr<float>();
+    a.lse_stride_h = lse.stride(0);
+  }
+  const size_t ws_bytes = ifa4_decode_paged_workspace_bytes(&a, &kv);
+  if (ws_bytes == 0 && a.batch > 0)  // invalid arguments: the call reports which status
+    check_status(ifa4_decode_paged_fwd(&a, &kv, nullptr, 0, nullptr), "decode_paged");
+  at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes) + 256}, q.options().dtype(at::kByte));
+  const uintptr_t base = reinterpret_cast<uintptr_t>(ws.data_ptr());
+  void* aligned_ws = reinterpret_cast<void*>((base + 255) / 256 * 256);
+  const hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
+  check_status(ifa4_decode_paged_fwd(&a, &kv, aligned_ws, ws_bytes, stream), "decode_paged");
+  return {out, lse};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(inkling_fa4, m) {
@@ -167,9 +233,15 @@ TORCH_LIBRARY(inkling_fa4, m) {
       "decode(Tensor q, Tensor k, Tensor v, Tensor rel_logits, Tensor cu_seqlens_q, "
       "Tensor cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, int rel_extent, bool causal, "
       "int window_left, float softmax_scale, bool return_lse, int flags) -> (Tensor, Tensor)");
+  m.def(
+      "decode_paged(Tensor q, Tensor k_cache, Tensor v_cache, Tensor rel_logits, "
+      "Tensor cu_seqlens_q, Tensor seqused_k, Tensor block_table, int max_seqlen_q, "
+      "int max_seqlen_k, int rel_extent, bool causal, int window_left, float softmax_scale, "
+      "bool return_lse) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(inkling_fa4, CUDA, m) {
   m.impl("fwd", &fwd);
   m.impl("decode", &decode);
+  m.impl("decode_paged", &decode_paged);
 }

@@ -2,12 +2,14 @@
 
 Same export names as the reference package (src/inkling_fa4/__init__.py:1-11),
 minus `ref_rel_attn`: the fp32 oracle is test infrastructure and lives in the
-repository's `oracle/` package, outside the product.
+repository's `oracle/` package, outside the product.  Added: the paged-KV
+decode entry point `inkling_fa4_rel_attention_decode_paged`.
 """
 from . import autotune_configs
 from .ops import (
     inkling_fa4_rel_attention,
     inkling_fa4_rel_attention_decode,
+    inkling_fa4_rel_attention_decode_paged,
     inkling_fa4_rel_attention_decode_triton,
     inkling_fa4_rel_attention_kv_pruned_triton,
     inkling_fa4_rel_attention_triton,
@@ -17,6 +19,7 @@ from .ops import (
 __all__ = [
     "inkling_fa4_rel_attention",
     "inkling_fa4_rel_attention_decode",
+    "inkling_fa4_rel_attention_decode_paged",
     "inkling_fa4_rel_attention_triton",
     "inkling_fa4_rel_attention_decode_triton",
     "inkling_fa4_rel_attention_kv_pruned_triton",

@@ -8,7 +8,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libifa4.so")
+# Same override as the torch binding loader (_native.py): a sweep variant directory.
+LIB_PATH = os.path.join(os.environ.get("IFA4_LIB_DIR", _HERE), "libifa4.so")
 
 IFA4_OK = 0
 IFA4_EINVAL = 1
@@ -56,7 +57,18 @@ class Ifa4Tile(ctypes.Structure):
                 ("stages", _c_int32), ("kv_chunk", _c_int32)]
 
 
+class Ifa4PagedKV(ctypes.Structure):
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32), ("block_size", _c_int32),
+        ("block_table", _vp), ("seqused_k", _vp),
+        ("block_table_stride", _c_int64), ("k_stride_block", _c_int64),
+        ("v_stride_block", _c_int64),
+        ("num_blocks", _c_int32), ("max_blocks_per_seq", _c_int32),
+    ]
+
+
 _P_ARGS = ctypes.POINTER(Ifa4Args)
+_P_PAGED = ctypes.POINTER(Ifa4PagedKV)
 _P_TILE = ctypes.POINTER(Ifa4Tile)
 _P_I32 = ctypes.POINTER(ctypes.c_int32)
 _P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -71,6 +83,8 @@ SIGNATURES = {
     "ifa4_decode_workspace_bytes": (ctypes.c_size_t, [_P_ARGS]),
     "ifa4_decode_tile": (_c_int32, [_P_ARGS, _P_TILE]),
     "ifa4_decode_fwd": (_c_int32, [_P_ARGS, _vp, ctypes.c_size_t, _vp]),
+    "ifa4_decode_paged_workspace_bytes": (ctypes.c_size_t, [_P_ARGS, _P_PAGED]),
+    "ifa4_decode_paged_fwd": (_c_int32, [_P_ARGS, _P_PAGED, _vp, ctypes.c_size_t, _vp]),
 }
 
 _lib = None
@@ -107,6 +121,15 @@ def make_args(**kw):
     for k, v in kw.items():
         setattr(a, k, v)
     return a
+
+
+def make_paged(**kw):
+    """Ifa4PagedKV with struct_size filled, fields from kw."""
+    kv = Ifa4PagedKV()
+    kv.struct_size = ctypes.sizeof(Ifa4PagedKV)
+    for k, v in kw.items():
+        setattr(kv, k, v)
+    return kv
 
 
 def prefill_tile(head_dim):

@@ -8,7 +8,10 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-EXT_PATH = os.path.join(_HERE, "_ifa4_torch.so")
+# IFA4_LIB_DIR: load the native pair (_ifa4_torch.so, libifa4.so) from another
+# directory, e.g. one variant build of a tile sweep (inkling_fa4.sweep).
+LIB_DIR = os.environ.get("IFA4_LIB_DIR", _HERE)
+EXT_PATH = os.path.join(LIB_DIR, "_ifa4_torch.so")
 _loaded = False
 
 
@@ -27,4 +30,4 @@ def ops():
 
 def loaded_paths():
     """Native libraries this module loads (for provenance checks)."""
-    return [EXT_PATH, os.path.join(_HERE, "libifa4.so")]
+    return [EXT_PATH, os.path.join(LIB_DIR, "libifa4.so")]

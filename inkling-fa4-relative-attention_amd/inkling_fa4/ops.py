@@ -7,7 +7,9 @@ signatures:
   inkling_fa4_rel_attention_kv_pruned_triton  src/inkling_fa4/triton_kernel_kv_pruned.py:210-279
   inkling_fa4_rel_attention_decode_triton     src/inkling_fa4/triton_kernel_decode.py:127-170
 
-plus the same entry points under names without the `_triton` suffix.
+plus the same entry points under names without the `_triton` suffix, and
+`inkling_fa4_rel_attention_decode_paged` for a paged KV cache (block tables),
+the format of the serving caller (outputs/architecture.md:117-120).
 
 Differences from the reference wrappers (all deliberate):
   * one kernel launch for the whole batch and no host synchronisation (the
@@ -101,6 +103,32 @@ def inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqle
     out, lse = _ops().decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
                              int(max_seqlen_q), int(max_seqlen_k), int(rel_extent), bool(causal),
                              _window_left(window_size), scale, bool(return_lse), 0)
+    return (out, lse) if return_lse else out
+
+
+@torch.no_grad()
+def inkling_fa4_rel_attention_decode_paged(q, k_cache, v_cache, rel_logits, cu_seqlens_q,
+                                           seqused_k, block_table, max_seqlen_q, max_seqlen_k,
+                                           rel_extent, causal=True, window_size=(-1, -1), *,
+                                           softmax_scale=None, return_lse=False):
+    """Decode over a paged KV cache (the serving backend's format,
+    outputs/architecture.md:117-120: blocks of 16 tokens).
+
+    k_cache / v_cache [num_blocks, block_size, Hkv, D] (block_size a power of
+    two >= 8, last dim contiguous), block_table int32 [batch, max_blocks]
+    (sequence b's key j sits in block block_table[b, j // block_size] at row
+    j % block_size), seqused_k int32 [batch] keys per sequence; one query per
+    sequence (cu_seqlens_q == arange(batch + 1)), GQA groups up to 16.
+    Results equal inkling_fa4_rel_attention_decode on the same keys stored
+    contiguously (bit for bit).  max_seqlen_k must bound seqused_k.
+    """
+    if k_cache.dim() != 4:
+        raise ValueError("k_cache must be [num_blocks, block_size, kv_heads, head_dim]")
+    scale = _resolve(q, k_cache[0], None, None, None, softmax_scale)
+    out, lse = _ops().decode_paged(q, k_cache, v_cache, rel_logits, cu_seqlens_q, seqused_k,
+                                   block_table, int(max_seqlen_q), int(max_seqlen_k),
+                                   int(rel_extent), bool(causal), _window_left(window_size),
+                                   scale, bool(return_lse))
     return (out, lse) if return_lse else out
 
 

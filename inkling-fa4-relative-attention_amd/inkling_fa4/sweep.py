@@ -1,0 +1,226 @@
+"""Tile sweep of the gfx950 kernels: build variants over compile-time knobs,
+check each against the in-tree build, time it on the GPU, optionally with
+rocprofv3 counters.
+
+Replaces the reference's benchmarks/autotune.py:21-81, an exhaustive
+BLOCK_Q/BLOCK_K/warps/stages timing loop whose launches pass out=None with zero
+output strides (autotune.py:74,78), so its numbers cannot be trusted.
+
+Two steps, so that variants are built where hipcc is and timed where the GPU is:
+
+  python -m inkling_fa4.sweep build --dir DIR --grid IFA4_LOOK_K=2,4,6 --grid IFA4_PRIO=0,1
+  python -m inkling_fa4.sweep run --dir DIR --workload prefill [--seq 4096] [--steps 30]
+        [--counters SQ_VALU_MFMA_BUSY_CYCLES,GRBM_GUI_ACTIVE] [--out table.md]
+
+`build` writes one sub-directory per grid point holding libifa4.so, a copy of the
+torch binding (it loads the libifa4.so next to it) and knobs.json.  `run` first
+runs the in-tree build, then each variant in a child process with IFA4_LIB_DIR
+pointing at its directory; a variant whose output on a small case differs from
+the in-tree build's (atol 2e-2 on out, 1e-3 on lse) is reported and not timed.
+
+Knobs (macros of the kernel sources):
+  prefill_fwd.hip  IFA4_LOOK_K, IFA4_LOOK_V   LDS reads in flight ahead of the QK / PV MFMAs
+                   IFA4_PRIO                  raised wave priority around MFMA blocks (0/1)
+                   IFA4_SCHED                 scheduling groups (0/1)
+                   IFA4_PV2                   key-block-major PV (0/1)
+                   IFA4_BIAS_LDS              shared bias table in LDS (0/1)
+                   IFA4_PREFILL_NQB           32-row blocks per wave (1/2)
+  tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
+"""
+import argparse
+import itertools
+import json
+import os
+import shutil
+import sqlite3
+import subprocess
+import sys
+import tempfile
+import time
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_PKG_ROOT = os.path.dirname(_HERE)  # inkling-fa4-relative-attention_amd/
+
+
+def _grid_points(specs):
+    """['A=1,2', 'B=x'] -> [{'A': '1', 'B': 'x'}, {'A': '2', 'B': 'x'}]"""
+    names, values = [], []
+    for spec in specs:
+        name, _, vals = spec.partition("=")
+        if not name or not vals:
+            raise SystemExit(f"bad --grid {spec!r}: expected NAME=v1,v2,...")
+        names.append(name)
+        values.append(vals.split(","))
+    return [dict(zip(names, combo)) for combo in itertools.product(*values)]
+
+
+def cmd_build(args):
+    sys.path.insert(0, _PKG_ROOT)
+    import build as b  # inkling-fa4-relative-attention_amd/build.py
+
+    ext = os.path.join(_HERE, b.EXT_NAME)
+    if not os.path.exists(ext):
+        raise SystemExit(f"{ext} is missing: build the package first (build.py)")
+    os.makedirs(args.dir, exist_ok=True)
+    for knobs in _grid_points(args.grid):
+        name = "_".join(f"{k.replace('IFA4_', '').lower()}{v}" for k, v in knobs.items())
+        out = os.path.join(args.dir, name)
+        with tempfile.TemporaryDirectory() as tmp:
+            b.build_library(args.jobs, out_dir=out,
+                            defines=[f"{k}={v}" for k, v in knobs.items()], build_dir=tmp)
+        shutil.copy2(ext, os.path.join(out, b.EXT_NAME))
+        with open(os.path.join(out, "knobs.json"), "w") as f:
+            json.dump(knobs, f)
+        print(f"built {out}  {knobs}", flush=True)
+    return 0
+
+
+def _case(workload, seq):
+    from inkling_fa4 import testing
+
+    if workload == "prefill":
+        return testing.ragged_varlen(), testing.long_prefill(seq, batch=8)
+    return testing.decode(batch=8, seed=21, causal=False), testing.decode(causal=False)
+
+
+def _call(workload, case, return_lse):
+    from inkling_fa4 import inkling_fa4_rel_attention, inkling_fa4_rel_attention_decode
+
+    fn = inkling_fa4_rel_attention if workload == "prefill" else inkling_fa4_rel_attention_decode
+    args = case.args()
+    return lambda: fn(*args, causal=case.causal, window_size=case.window_size,
+                      softmax_scale=case.scale, return_lse=return_lse)
+
+
+def cmd_measure(args):
+    """Child process: small-case output to args.check_out, then the timing (JSON)."""
+    import torch
+
+    small, big = (c.to("cuda") for c in _case(args.workload, args.seq))
+    if args.check_out:  # skipped under counters: only the timed workload's dispatches count
+        out, lse = _call(args.workload, small, True)()
+        torch.save({"out": out.cpu(), "lse": lse.cpu()}, args.check_out)
+    fn = _call(args.workload, big, False)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < args.settle:  # settle the clocks
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(args.steps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    print(json.dumps({"ms": a.elapsed_time(b) / args.steps}))
+    return 0
+
+
+def _counters(db, kernel_prefix):
+    con = sqlite3.connect(db)
+    rows = con.execute("select kernel_name, counter_name, avg(value) from counters_collection "
+                       "group by kernel_name, counter_name")
+    return {cn: v for k, cn, v in rows if kernel_prefix in k}
+
+
+def cmd_run(args):
+    import torch
+
+    variants = [("in-tree", None, {})]
+    for name in sorted(os.listdir(args.dir)):
+        d = os.path.join(args.dir, name)
+        if os.path.exists(os.path.join(d, "knobs.json")):
+            with open(os.path.join(d, "knobs.json")) as f:
+                variants.append((name, d, json.load(f)))
+    kernel = "prefill_fwd_kernel" if args.workload == "prefill" else "decode_stream_kernel"
+    rows, ref = [], None
+    with tempfile.TemporaryDirectory() as tmp:
+        for name, d, knobs in variants:
+            env = dict(os.environ)
+            env.pop("IFA4_LIB_DIR", None)
+            if d is not None:
+                env["IFA4_LIB_DIR"] = os.path.abspath(d)
+            check = os.path.join(tmp, f"{name}.pt")
+            child = [sys.executable, "-m", "inkling_fa4.sweep", "measure", "--workload",
+                     args.workload, "--seq", str(args.seq), "--steps", str(args.steps),
+                     "--warmup", str(args.warmup), "--settle", str(args.settle),
+                     "--check-out", check]
+            res = subprocess.run(child, env=env, cwd=_PKG_ROOT, capture_output=True, text=True,
+                                 timeout=args.timeout)
+            if res.returncode != 0:
+                rows.append((name, knobs, None, "failed to run", {}))
+                print(f"{name}: failed\n{res.stderr[-2000:]}", file=sys.stderr, flush=True)
+                continue
+            got = torch.load(check, weights_only=True)
+            verdict = "reference"
+            if ref is None:
+                ref = got
+            else:
+                ok = (torch.allclose(got["out"].float(), ref["out"].float(), atol=2e-2, rtol=2e-2)
+                      and torch.allclose(got["lse"], ref["lse"], atol=1e-3, rtol=0))
+                verdict = "agrees" if ok else "DIFFERS (not timed)"
+                if not ok:
+                    rows.append((name, knobs, None, verdict, {}))
+                    continue
+            ms = json.loads(res.stdout.strip().splitlines()[-1])["ms"]
+            cnt = {}
+            if args.counters:
+                pmc_dir = os.path.join(tmp, f"pmc_{name}")
+                # counters on a short run: every dispatch is serialised under --pmc
+                short = child[:child.index("--steps")] + [
+                    "--steps", "3", "--warmup", "1", "--settle", "0", "--check-out", ""]
+                prof = ["rocprofv3", "--pmc"] + args.counters.split(",") + \
+                       ["-d", pmc_dir, "-o", "run", "--"] + short
+                pr = subprocess.run(prof, env=env, cwd=_PKG_ROOT, capture_output=True, text=True,
+                                    timeout=args.timeout)
+                db = os.path.join(pmc_dir, "run_results.db")
+                if pr.returncode == 0 and os.path.exists(db):
+                    cnt = _counters(db, kernel)
+            rows.append((name, knobs, ms, verdict, cnt))
+            print(f"{name}: {ms:.4f} ms {verdict} {cnt}", flush=True)
+    names = sorted({c for r in rows for c in r[4]})
+    lines = [f"| variant | knobs | ms | check | " + " | ".join(names) + " |",
+             "|---|---|---|---|" + "---|" * len(names)]
+    for name, knobs, ms, verdict, cnt in rows:
+        ms_s = f"{ms:.4f}" if ms is not None else "—"
+        lines.append(f"| {name} | {json.dumps(knobs)} | {ms_s} | {verdict} | " +
+                     " | ".join(f"{cnt[c]:.4g}" if c in cnt else "—" for c in names) + " |")
+    table = "\n".join(lines)
+    print(table)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(table + "\n")
+    return 0
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(prog="python -m inkling_fa4.sweep")
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    b = sub.add_parser("build")
+    b.add_argument("--dir", required=True)
+    b.add_argument("--grid", action="append", required=True, help="NAME=v1,v2,...")
+    b.add_argument("--jobs", type=int, default=4)
+    for name in ("run", "measure"):
+        r = sub.add_parser(name)
+        r.add_argument("--workload", choices=["prefill", "decode"], default="prefill")
+        r.add_argument("--seq", type=int, default=4096)
+        r.add_argument("--steps", type=int, default=30)
+        r.add_argument("--warmup", type=int, default=5)
+        r.add_argument("--settle", type=float, default=0.5, help="seconds of untimed calls first")
+        if name == "run":
+            r.add_argument("--dir", required=True)
+            r.add_argument("--counters", default="")
+            r.add_argument("--out", default="")
+            r.add_argument("--timeout", type=int, default=300)
+        else:
+            r.add_argument("--check-out", default="",
+                           help="file for the small-case output ('' = no check case)")
+    args = ap.parse_args(argv)
+    return {"build": cmd_build, "run": cmd_run, "measure": cmd_measure}[args.cmd](args)
+
+
+if __name__ == "__main__":
+    sys.exit(main())

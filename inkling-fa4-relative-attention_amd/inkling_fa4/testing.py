@@ -135,3 +135,48 @@ def decode(seed=5, batch=64, dtype=torch.bfloat16, causal=False, scale=None, lo=
     g, lens = decode_lengths(batch, seed, lo, hi)
     return make_case("decode", [1] * batch, lens, 8, 2, 128, dtype, seed=seed, causal=causal,
                      scale=scale, gen=g)
+
+
+@dataclass
+class PagedKV:
+    """A paged copy of a case's K/V: k_cache / v_cache [num_blocks, block_size,
+    Hkv, D], block_table int32 [batch, max_blocks], seqused_k int32 [batch]."""
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    block_table: torch.Tensor
+    seqused_k: torch.Tensor
+
+    def to(self, device):
+        return PagedKV(*(t.to(device) for t in (self.k_cache, self.v_cache, self.block_table,
+                                                 self.seqused_k)))
+
+
+def paginate(case, block_size=16, seed=0, spare_blocks=5, fill=float("nan"),
+             unused_entry=1 << 30, extra_columns=0):
+    """Store the case's K/V in a block pool: the sequences' blocks in a seeded
+    random physical order, `spare_blocks` unreferenced blocks, and every row no
+    sequence owns (spare blocks, rows past a sequence's end) set to `fill`.
+    Table entries past a sequence's last block hold `unused_entry`;
+    `extra_columns` widens the table beyond what the longest sequence needs."""
+    g = torch.Generator().manual_seed(seed)
+    cu = [int(x) for x in case.cu_k.tolist()]
+    lens = [cu[b + 1] - cu[b] for b in range(len(cu) - 1)]
+    nblk = [(n + block_size - 1) // block_size for n in lens]
+    max_blocks = max([1] + nblk) + extra_columns
+    total = sum(nblk) + spare_blocks
+    phys = torch.randperm(max(total, 1), generator=g).tolist()
+    hkv, d = case.k.shape[1], case.k.shape[2]
+    kc = torch.full((max(total, 1), block_size, hkv, d), fill, dtype=case.k.dtype)
+    vc = torch.full_like(kc, fill)
+    table = torch.full((len(lens), max_blocks), unused_entry, dtype=torch.int32)
+    nxt = 0
+    for b, n in enumerate(lens):
+        for j in range(nblk[b]):
+            blk = phys[nxt]
+            nxt += 1
+            table[b, j] = blk
+            rows = min(block_size, n - j * block_size)
+            src = cu[b] + j * block_size
+            kc[blk, :rows] = case.k[src:src + rows]
+            vc[blk, :rows] = case.v[src:src + rows]
+    return PagedKV(kc, vc, table, torch.tensor(lens, dtype=torch.int32))

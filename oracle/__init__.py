@@ -11,6 +11,10 @@ Contents
                  log-sum-exp the reference does not return.
   merge.py       closed-form log-sum-exp merge of split partials (the
                  split-KV decode combine; no reference counterpart).
+  paged.py       paged KV cache (block tables) -> contiguous varlen K/V, and
+                 the oracle over a paged cache (the serving format of
+                 outputs/architecture.md:117-120; no kernel counterpart in
+                 the reference).
 
 How each function is pinned (see tests/test_oracle_*.py):
   ref_rel_attn   golden vectors written by tests/golden/make_golden.py from
@@ -24,6 +28,10 @@ How each function is pinned (see tests/test_oracle_*.py):
                  library routine) and sum_j exp(s_ij - lse_i) == 1.
   merge_partials split-count invariance (1, 2, 7 and one split per key) and
                  equality with the unsplit oracle.
+  gather_paged   identity tables reproduce the contiguous cache; invariance
+                 under physical block permutation and block size; rows no
+                 sequence owns (NaN-filled) never reach the result.
 """
 from .reference import ref_rel_attn, ref_rel_attn_with_lse  # noqa: F401
 from .merge import merge_partials  # noqa: F401
+from .paged import gather_paged, ref_rel_attn_paged_with_lse  # noqa: F401

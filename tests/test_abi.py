@@ -198,3 +198,59 @@ def test_chunked_window_workload_tile_counts():
     cu_k = [384 * b for b in range(17)]
     visited, total = _abi.count_tiles(cu_q, cu_k, 8, causal=True, window_left=63)
     assert (visited, total) == (16 * 8 * 2, 16 * 8 * 6)
+
+
+def _paged_ok(**kw):
+    base = dict(block_size=16, block_table=8 * _P, seqused_k=9 * _P, block_table_stride=1024,
+                k_stride_block=16 * 2 * 128, v_stride_block=16 * 2 * 128, num_blocks=40000,
+                max_blocks_per_seq=1024)
+    base.update(kw)
+    return _abi.make_paged(**base)
+
+
+def _decode_args(**kw):
+    base = dict(batch=64, total_q=64, max_seqlen_q=1, max_seqlen_k=16384, causal=0,
+                cu_seqlens_k=0, total_k=0)
+    base.update(kw)
+    return _good(**base)
+
+
+@pytest.mark.parametrize("kw,expect", [
+    ({}, _abi.IFA4_OK),
+    ({"block_size": 8}, _abi.IFA4_EINVAL),           # 1024 blocks of 8 < 16384 keys
+    ({"block_size": 8, "max_blocks_per_seq": 2048}, _abi.IFA4_OK),
+    ({"block_size": 12}, _abi.IFA4_EINVAL),          # not a power of two
+    ({"block_size": 4, "max_blocks_per_seq": 4096}, _abi.IFA4_EINVAL),
+    ({"block_size": 1 << 17}, _abi.IFA4_EINVAL),
+    ({"block_table": 0}, _abi.IFA4_EINVAL),
+    ({"seqused_k": 0}, _abi.IFA4_EINVAL),
+    ({"seqused_k": 9 * _P + 2}, _abi.IFA4_EINVAL),
+    ({"num_blocks": 0}, _abi.IFA4_EINVAL),
+    ({"max_blocks_per_seq": 1023}, _abi.IFA4_EINVAL),  # cannot address max_seqlen_k
+    ({"k_stride_block": 16 * 2 * 128 + 4}, _abi.IFA4_EUNSUPPORTED),
+    ({"block_table_stride": -1}, _abi.IFA4_EINVAL),
+    ({"block_table_stride": 0}, _abi.IFA4_OK),        # every sequence shares one row
+    ({"struct_size": 8}, _abi.IFA4_EINVAL),
+])
+def test_paged_validation(kw, expect):
+    lib = _abi.lib()
+    a = _decode_args()
+    kv = _paged_ok(**kw)
+    ws = lib.ifa4_decode_paged_workspace_bytes(ctypes.byref(a), ctypes.byref(kv))
+    # the workspace query accepts exactly the valid descriptions; a valid call
+    # without workspace stops at the workspace check, an invalid one before it
+    assert (ws > 0) == (expect == _abi.IFA4_OK)
+    st = lib.ifa4_decode_paged_fwd(ctypes.byref(a), ctypes.byref(kv), None, 0, None)
+    assert st == (_abi.IFA4_EWORKSPACE if expect == _abi.IFA4_OK else expect)
+
+
+def test_paged_workspace_equals_contiguous_workspace():
+    lib = _abi.lib()
+    a = _decode_args()
+    contiguous = _decode_args(cu_seqlens_k=7 * _P, total_k=600000)
+    assert lib.ifa4_decode_paged_workspace_bytes(ctypes.byref(a), ctypes.byref(_paged_ok())) == \
+        lib.ifa4_decode_workspace_bytes(ctypes.byref(contiguous))
+    # the contiguous entry points still need cu_seqlens_k
+    assert lib.ifa4_decode_workspace_bytes(ctypes.byref(a)) == 0
+    assert lib.ifa4_decode_paged_fwd(ctypes.byref(a), None, 256, 1 << 30, None) == \
+        _abi.IFA4_EINVAL
