@@ -46,8 +46,18 @@ typedef enum ifa4_dtype {
   IFA4_FP32 = 2
 } ifa4_dtype;
 
-/* Debug flags (ifa4_args.flags). */
-#define IFA4_FLAG_NO_PRUNE 0x1u  /* visit every KV tile (pruning-invariance tests) */
+/* Flags (ifa4_args.flags). */
+#define IFA4_FLAG_NO_PRUNE 0x1u  /* debug: visit every KV tile (pruning-invariance tests) */
+/*
+ * Bottom-right alignment, the convention of upstream flash-attn and of the
+ * serving backend's score_mod (outputs/architecture.md:72, d = (i + sk - sq) - j):
+ * query i sits at key position i + (Lk - Lq), so
+ *   dist = i + (Lk - Lq) - j,  causal keeps j <= i + (Lk - Lq),
+ *   the window keeps i + (Lk - Lq) - j <= window_left.
+ * Without the flag the semantics are the reference oracle's (top-left, above).
+ * The two agree when Lq == Lk.
+ */
+#define IFA4_FLAG_BOTTOM_RIGHT 0x2u
 
 /*
  * Arguments of one forward call.  Layouts (element strides, last dim contiguous):

@@ -4,10 +4,12 @@
 // (src/inkling_fa4/triton_kernel_decode.py:22-124,127-170).  Semantics follow
 // the reference oracle (src/inkling_fa4/reference.py:19-40) for Lq = 1:
 // query local index i = 0, dist = (1 - Lk) - j, causal keeps j <= 0 only, and
-// the left window never masks (i - j <= 0).
+// the left window never masks (i - j <= 0).  With bottom-right alignment
+// (IFA4_FLAG_BOTTOM_RIGHT) the query sits at key Lk - 1: dist = (Lk - 1) - j,
+// causal keeps every key, the window keeps j >= Lk - 1 - window_left.
 //
-// Work decomposition.  A "segment" is one (sequence, kv head); it holds
-// ceil(kend / 32) steps of 32 keys.  All segments' steps are laid end to end
+// Work decomposition.  A "segment" is one (sequence, kv head); it holds the
+// 32-key steps of its visible keys (decode_keys).  All segments' steps are laid end to end
 // (sequence-major, kv head minor) and W persistent waves (about one resident
 // round on the chip) each take an equal contiguous range of P = ceil(T / W)
 // steps.  A wave therefore streams K/V without gaps across segment
@@ -63,10 +65,33 @@ struct DecodeQ {
   static constexpr int kElems = 512 * kDma;
 };
 
-// Steps of a sequence: 32-key steps over its visible keys, 0 when it does not
+// Visible keys [kbeg, kend) of the single query of a sequence with lk keys.
+// Top-left (the reference oracle): causal keeps key 0 only, the left window
+// never masks (i - j <= 0).  Bottom-right: query 0 sits at key lk - 1, so
+// causal keeps every key and the window keeps keys >= lk - 1 - window_left.
+// Steps start at the 32-key boundary kfirst <= kbeg (keys below kbeg are
+// masked), so a step never straddles a 32-key boundary of the sequence.
+struct KeyRange {
+  int kbeg, kfirst, kend;
+};
+__device__ __forceinline__ KeyRange decode_keys(const DecodeParams& p, int lk) {
+  KeyRange r;
+  if (p.bottom_right) {
+    r.kend = lk;
+    r.kbeg = p.window_left >= 0 ? max(0, lk - 1 - p.window_left) : 0;
+  } else {
+    r.kend = p.causal ? min(lk, 1) : lk;
+    r.kbeg = 0;
+  }
+  r.kfirst = r.kbeg & ~(kStep - 1);
+  return r;
+}
+
+// Steps of a sequence: 32-key steps over [kfirst, kend), 0 when it does not
 // hold exactly one query.
-__device__ __forceinline__ int seq_steps(int lq, int kend) {
-  return (lq == 1 && kend > 0) ? (kend + kStep - 1) / kStep : 0;
+__device__ __forceinline__ int seq_steps(int lq, const KeyRange& r) {
+  const int n = r.kend - r.kfirst;
+  return (lq == 1 && n > 0) ? (n + kStep - 1) / kStep : 0;
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave.
@@ -83,7 +108,7 @@ __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
 struct SeqChunk {
   int base;        // first sequence of the chunk (wave-uniform)
   int total_incl;  // steps of all sequences up to the end of the chunk (uniform)
-  int steps, excl, qs, ks, kend, lk;  // this lane's sequence
+  int steps, excl, qs, ks, kbeg, kend, lk;  // this lane's sequence
 };
 
 // Keys of sequence `seq` in a paged cache: seqused_k clamped to what the
@@ -100,7 +125,7 @@ __device__ __forceinline__ SeqChunk load_chunk(const DecodeParams& p, int base, 
   c.base = base;
   const int seq = base + lane;
   c.steps = 0;
-  c.qs = c.ks = c.kend = c.lk = 0;
+  c.qs = c.ks = c.kbeg = c.kend = c.lk = 0;
   if (seq < p.batch) {
     c.qs = p.cu_q[seq];
     const int lq = p.cu_q[seq + 1] - c.qs;
@@ -110,8 +135,10 @@ __device__ __forceinline__ SeqChunk load_chunk(const DecodeParams& p, int base, 
       c.ks = p.cu_k[seq];
       c.lk = p.cu_k[seq + 1] - c.ks;
     }
-    c.kend = p.causal ? min(c.lk, 1) : c.lk;
-    c.steps = seq_steps(lq, c.kend);
+    const KeyRange kr = decode_keys(p, c.lk);
+    c.kbeg = kr.kbeg;
+    c.kend = kr.kend;
+    c.steps = seq_steps(lq, kr);
   }
   const int incl = wave_incl_scan(c.steps, lane);
   c.excl = excl0 + incl - c.steps;
@@ -124,10 +151,15 @@ struct Cursor {
   int seq, kvh, step, steps;  // step within the segment, steps of the segment
   int seg;                    // seq * kv_heads + kvh
   int seg_g0;                 // global index of the segment's first step
-  int qs, ks, kend, lk;
+  int qs, ks, kbeg, kend, lk;  // keys [kbeg, kend) visible; steps from kbeg & ~31
   int slot;                   // Q slot of the segment (0 / 1)
   bool first;                 // first step of the segment in this wave
 };
+
+// First key of the cursor's step (a multiple of 32).
+__device__ __forceinline__ int step_key0(const Cursor& cu) {
+  return (cu.kbeg & ~(kStep - 1)) + cu.step * kStep;
+}
 
 template <int D, typename Tag, int G, bool kPaged>
 __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
@@ -181,6 +213,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
         cu.seg_g0 = hkv * excl + cu.kvh * cu.steps;
         cu.qs = __builtin_amdgcn_readlane(ch.qs, L);
         cu.ks = __builtin_amdgcn_readlane(ch.ks, L);
+        cu.kbeg = __builtin_amdgcn_readlane(ch.kbeg, L);
         cu.kend = __builtin_amdgcn_readlane(ch.kend, L);
         cu.lk = __builtin_amdgcn_readlane(ch.lk, L);
         cu.slot = 0;
@@ -205,7 +238,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
   int tw = -1, tw_seq = -1, tw_base = 0;
   const int bmask = (1 << p.block_shift) - 1;
   auto load_paged = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu) {
-    const int k0 = cu.step * kStep;
+    const int k0 = step_key0(cu);
     const int blk0 = k0 >> p.block_shift;
     if (cu.seq != tw_seq || blk0 < tw_base || blk0 >= tw_base + 64) {
       tw_seq = cu.seq;
@@ -251,7 +284,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
           make_rsrc_uniform(kbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.k_st + D) * 2));
       const rsrc_t rv =
           make_rsrc_uniform(vbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.v_st + D) * 2));
-      const int k0 = cu.step * kStep;
+      const int k0 = step_key0(cu);
 #pragma unroll
       for (int i = 0; i < S::kLoads; ++i) {
         const uint32_t row = (uint32_t)(k0 + S::kRpi * i + r);
@@ -323,10 +356,10 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
         acc[blk] = E::mfma16(*reinterpret_cast<const u32x4_t*>(krow + 32 * kk), qf[kk], acc[blk]);
     }
 
-    const int k0 = cu.step * kStep;
+    const int k0 = step_key0(cu);
     const int c1 = cu.kend;
-    const int delta = 1 - cu.lk;
-    const bool tail = k0 + kStep > c1;
+    const int delta = p.bottom_right ? cu.lk - 1 : 1 - cu.lk;  // dist = delta - key (i = 0)
+    const bool tail = k0 + kStep > c1 || k0 < cu.kbeg;
     const bool bias = delta - k0 >= 0;  // some key of the step has dist >= 0
     float mx = -INFINITY;
 #pragma unroll
@@ -343,7 +376,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
                           p.rel_dtype) *
                  kLog2e;
           }
-          if (key >= c1) x = -INFINITY;
+          if (key >= c1 || key < cu.kbeg) x = -INFINITY;
         }
         acc[blk][j] = x;
         mx = fmaxf(mx, x);
@@ -511,9 +544,8 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
   const int meta_first = p.ws_meta[2 * seg];  // read before knowing it is needed
   const int meta_last = p.ws_meta[2 * seg + 1];
   if (lq != 1) return;
-  const int kend = p.causal ? min(lk, 1) : lk;
   int w_first = 0, parts = 0;
-  if (seq_steps(lq, kend) > 0 && p.n_waves > 0) {
+  if (seq_steps(lq, decode_keys(p, lk)) > 0 && p.n_waves > 0) {
     // clamped so that a slot index can never leave the workspace
     w_first = min(max(meta_first, 0), p.n_waves - 1);
     parts = min(max(meta_last, w_first), p.n_waves - 1) - w_first + 1;

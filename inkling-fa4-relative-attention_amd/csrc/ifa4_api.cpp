@@ -134,6 +134,7 @@ ifa4::PrefillParams make_prefill_params(const ifa4_args* a) {
   p.rel_width = a->rel_width;
   p.window_left = a->window_left;
   p.causal = a->causal;
+  p.bottom_right = (a->flags & IFA4_FLAG_BOTTOM_RIGHT) ? 1 : 0;
   p.no_prune = (a->flags & IFA4_FLAG_NO_PRUNE) ? 1 : 0;
   p.rel_dtype = a->rel_dtype;
   const int bq = ifa4::prefill_block_q();
@@ -142,8 +143,13 @@ ifa4::PrefillParams make_prefill_params(const ifa4_args* a) {
   return p;
 }
 
+// Top-left causal decode (Lq = 1) sees key 0 only.
+bool key0_only(const ifa4_args* a) {
+  return a->causal != 0 && (a->flags & IFA4_FLAG_BOTTOM_RIGHT) == 0;
+}
+
 int32_t decode_waves(const ifa4_args* a) {
-  return ifa4::decode_waves_for(a->batch, a->kv_heads, a->max_seqlen_k, a->causal != 0);
+  return ifa4::decode_waves_for(a->batch, a->kv_heads, a->max_seqlen_k, key0_only(a));
 }
 
 // Decode workspace: partial (o, lse) slots, one per (segment, wave) pair that
@@ -211,6 +217,8 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, void* workspa
   p.group = args->n_heads / args->kv_heads;
   p.rel_extent = args->rel_extent;
   p.causal = args->causal;
+  p.bottom_right = (args->flags & IFA4_FLAG_BOTTOM_RIGHT) ? 1 : 0;
+  p.window_left = args->window_left;
   p.rel_dtype = args->rel_dtype;
   p.n_waves = decode_waves(args);
   p.scale_log2 = args->softmax_scale * kLog2eHost;
@@ -282,17 +290,22 @@ int32_t ifa4_prefill_count_tiles(const ifa4_args* args, const int32_t* cu_q, con
   const int bq = ifa4::prefill_block_q();
   const int bk = ifa4::prefill_block_k();
   const bool no_prune = (args->flags & IFA4_FLAG_NO_PRUNE) != 0;
+  const bool bottom_right = (args->flags & IFA4_FLAG_BOTTOM_RIGHT) != 0;
   int64_t vis = 0, tot = 0;
   for (int b = 0; b < args->batch; ++b) {
     const int lq = cu_q[b + 1] - cu_q[b];
     const int lk = cu_k[b + 1] - cu_k[b];
     if (lq < 0 || lk < 0) return IFA4_EINVAL;
+    const int qpos = bottom_right ? lk - lq : 0;  // key position of query 0
     for (int q0 = 0; q0 < lq; q0 += bq) {
       const int q_hi = q0 + bq < lq ? q0 + bq : lq;
       int kend = lk, kbeg = 0;
       if (!no_prune) {
-        if (args->causal) kend = kend < q_hi ? kend : q_hi;
-        if (args->window_left >= 0) kbeg = q0 - args->window_left > 0 ? q0 - args->window_left : 0;
+        if (args->causal) kend = kend < q_hi + qpos ? kend : q_hi + qpos;
+        if (args->window_left >= 0) {
+          const int lo = q0 + qpos - args->window_left;
+          kbeg = lo > 0 ? lo : 0;
+        }
       }
       const int kt_beg = kbeg / bk;
       const int kt_end = kend > kbeg ? (kend + bk - 1) / bk : kt_beg;
@@ -321,7 +334,7 @@ int32_t ifa4_decode_tile(const ifa4_args* args, ifa4_tile* tile) {
   tile->waves = 1;
   tile->stages = 2;
   const int64_t steps = ifa4::decode_max_steps(args->batch, args->kv_heads, args->max_seqlen_k,
-                                               args->causal != 0);
+                                               key0_only(args));
   const int32_t w = decode_waves(args);
   tile->kv_chunk = w > 0 ? (int32_t)(((steps + w - 1) / w) * ifa4::kDecodeStep) : 0;
   return IFA4_OK;

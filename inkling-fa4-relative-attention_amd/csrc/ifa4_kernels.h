@@ -24,6 +24,7 @@ struct PrefillParams {
   int32_t rel_width;    // last dim of rel (>= rel_extent)
   int32_t window_left;  // -1: none
   int32_t causal;
+  int32_t bottom_right; // 1: query i sits at key position i + (lk - lq) (IFA4_FLAG_BOTTOM_RIGHT)
   int32_t no_prune;
   int32_t rel_dtype;    // 0 bf16, 1 fp16, 2 fp32
   int32_t n_qtiles;     // ceil(max_seqlen_q / block_q)
@@ -50,6 +51,8 @@ struct DecodeParams {
   int32_t group;
   int32_t rel_extent;
   int32_t causal;
+  int32_t bottom_right;  // see PrefillParams
+  int32_t window_left;   // -1: none (only matters with bottom_right: top-left decode never masks)
   int32_t rel_dtype;
   int32_t n_waves;   // persistent waves of pass 1 (0: nothing to stream)
   float scale_log2;

@@ -69,6 +69,12 @@
 #ifndef IFA4_PV2
 #define IFA4_PV2 1
 #endif
+#ifndef IFA4_ONEBAR
+#define IFA4_ONEBAR 1
+#endif
+#ifndef IFA4_PVALU
+#define IFA4_PVALU 7
+#endif
 
 namespace ifa4 {
 namespace {
@@ -173,7 +179,12 @@ void prefill_fwd_kernel(PrefillParams p) {
   const int q0 = qtile * kBlockQ;
   if (q0 >= lq) return;
   const int kvh = head / p.group;
-  const int delta = lq - lk;
+  // Query i sits at key position i + qpos for the causal and window masks;
+  // the bias distance is dist = i + delta - j.  Top-left (the reference
+  // oracle, src/inkling_fa4/reference.py:28-37): qpos = 0, delta = lq - lk.
+  // Bottom-right (upstream flash-attn): qpos = delta = lk - lq.
+  const int qpos = p.bottom_right ? lk - lq : 0;
+  const int delta = p.bottom_right ? lk - lq : lq - lk;
   const int wl = p.window_left;
   const int rext = p.rel_extent;
 
@@ -199,8 +210,8 @@ void prefill_fwd_kernel(PrefillParams p) {
   const int q_hi = min(q0 + kBlockQ, lq);  // exclusive
   int kend = lk, kbeg = 0;
   if (!p.no_prune) {
-    if (p.causal) kend = min(kend, q_hi);
-    if (wl >= 0) kbeg = max(0, q0 - wl);
+    if (p.causal) kend = min(kend, q_hi + qpos);
+    if (wl >= 0) kbeg = max(0, q0 + qpos - wl);
   }
   const int kt_beg = kbeg / kBlockK;
   const int kt_end = kend > kbeg ? (kend + kBlockK - 1) / kBlockK : kt_beg;
@@ -210,8 +221,8 @@ void prefill_fwd_kernel(PrefillParams p) {
   const int wrows = max(0, min(32 * kNqb, lq - qa));     // valid rows of the wave
   int wkend = lk, wkbeg = 0;
   if (!p.no_prune) {
-    if (p.causal) wkend = min(lk, qa + wrows);
-    if (wl >= 0) wkbeg = max(0, qa - wl);
+    if (p.causal) wkend = min(lk, qa + wrows + qpos);
+    if (wl >= 0) wkbeg = max(0, qa + qpos - wl);
   }
   int qi[kNqb];        // this lane's query (local) in each row block
   bool row_ok[kNqb];
@@ -285,8 +296,8 @@ void prefill_fwd_kernel(PrefillParams p) {
     if (!active) return;
     const int imin = qa, imax = qa + wrows - 1;
     const int jmin = kb, jmax = kb + kBlockK - 1;
-    const bool need_mask = jmax >= lk || (p.causal && jmax > imin) ||
-                           (wl >= 0 && imax - jmin > wl);
+    const bool need_mask = jmax >= lk || (p.causal && jmax > imin + qpos) ||
+                           (wl >= 0 && imax + qpos - jmin > wl);
     const bool has_bias =
         rext > 0 && (imax + delta - jmin >= 0) && (imin + delta - jmax <= rext - 1);
     const uint16_t* kl = stage;
@@ -362,9 +373,9 @@ void prefill_fwd_kernel(PrefillParams p) {
 #pragma unroll
       for (int qb = 0; qb < kNqb; ++qb) {
         int hi = lk - 1 - kb;
-        if (p.causal) hi = min(hi, qi[qb] - kb);
+        if (p.causal) hi = min(hi, qi[qb] + qpos - kb);
         if (!row_ok[qb]) hi = -1;
-        const int lo = wl >= 0 ? qi[qb] - wl - kb : -1;
+        const int lo = wl >= 0 ? qi[qb] + qpos - wl - kb : -1;
         const int hi_h = hi - 4 * half, lo_h = lo - 4 * half;
         const int dbase = qi[qb] + delta - kb - 4 * half;  // dist = dbase - kc
         const uint32_t rel_row_off = (uint32_t)(qi[qb] * p.rel_st) * Rel::kBytes;
@@ -485,7 +496,7 @@ void prefill_fwd_kernel(PrefillParams p) {
     // block's fragment and a share of the next block's exponentials.
     {
       constexpr int kT = kBlockK / 16;
-      constexpr int kPValu = 7;  // ~28 VALU/TRANS per block of P over 4 MFMAs
+      constexpr int kPValu = IFA4_PVALU;  // ~28 VALU/TRANS per block of P over 4 MFMAs
 #pragma unroll
       for (int t = 0; t < kT - 1; ++t) {
 #pragma unroll
@@ -565,11 +576,24 @@ void prefill_fwd_kernel(PrefillParams p) {
 #endif
 
   // ---- pipeline: DMA of tile kt+1 in flight while tile kt is computed -------------
-  // Per tile: issue the next DMA; wait until only that DMA is outstanding for
-  // this wave (its part of the current tile has landed); barrier (every wave's
-  // part has landed); compute; barrier (the stage may be overwritten next).
-  // The DMA is invisible to the compiler (dma_16), so these waits are the only
-  // ordering between a stage's DMA and its reads.
+  // The DMA is invisible to the compiler (dma_16), so these waits and barriers are
+  // the only ordering between a stage's DMA and its reads.
+#if IFA4_ONEBAR
+  // One barrier per tile: wait for this wave's part of tile kt (its DMA was
+  // issued a step earlier), barrier (every part landed, and every wave is done
+  // with tile kt-1, whose stage tile kt+1 now overwrites), then issue tile
+  // kt+1's DMA and compute tile kt.
+  auto step = [&](int kt, uint16_t* cur, uint16_t* nxt) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + 1 < kt_end) dma_tile(kt + 1, nxt);
+    compute(kt, cur);
+  };
+#else
+  // Two barriers per tile: issue tile kt+1's DMA; wait until only it is
+  // outstanding for this wave; barrier (every wave's part of tile kt landed);
+  // compute; barrier (the stage may be overwritten next).  1.4% slower.
   auto step = [&](int kt, uint16_t* cur, uint16_t* nxt) {
     if (kt + 1 < kt_end) {
       dma_tile(kt + 1, nxt);
@@ -583,6 +607,7 @@ void prefill_fwd_kernel(PrefillParams p) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
+#endif
   // The bias table (shared-table layout) is read with the Q fragments and the
   // first tile; one wait for all three, then it goes to LDS.  The first tile's
   // barrier publishes it.

@@ -38,15 +38,16 @@ constexpr int32_t kDecodeStep = 32;  // keys per step of a decode wave
 
 // Upper bound of the 32-key steps of a decode call: every (sequence, kv head)
 // at max_seqlen_k keys (one key when causal: top-left alignment, Lq = 1).
+// key0_only: top-left causal decode, which sees key 0 only.
 inline int64_t decode_max_steps(int64_t batch, int64_t kv_heads, int64_t max_seqlen_k,
-                                bool causal) {
-  const int64_t keys = causal ? (max_seqlen_k > 0 ? 1 : 0) : max_seqlen_k;
+                                bool key0_only) {
+  const int64_t keys = key0_only ? (max_seqlen_k > 0 ? 1 : 0) : max_seqlen_k;
   return batch * kv_heads * ((keys + kDecodeStep - 1) / kDecodeStep);
 }
 
 inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seqlen_k,
-                                bool causal) {
-  const int64_t t = decode_max_steps(batch, kv_heads, max_seqlen_k, causal);
+                                bool key0_only) {
+  const int64_t t = decode_max_steps(batch, kv_heads, max_seqlen_k, key0_only);
   return (int32_t)(t < kDecodeWaves ? t : kDecodeWaves);
 }
 

@@ -163,7 +163,7 @@ std::tuple<at::Tensor, at::Tensor> decode_paged(
     const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
     const at::Tensor& rel, const at::Tensor& cu_q, const at::Tensor& seqused_k,
     const at::Tensor& block_table, int64_t max_q, int64_t max_k, int64_t rel_extent, bool causal,
-    int64_t window_left, double softmax_scale, bool return_lse) {
+    int64_t window_left, double softmax_scale, bool return_lse, int64_t flags) {
   TORCH_CHECK(k_cache.dim() == 4 && v_cache.dim() == 4,
               "inkling_fa4.decode_paged: k_cache / v_cache must be "
               "[num_blocks, block_size, kv_heads, head_dim]");
@@ -185,7 +185,7 @@ std::tuple<at::Tensor, at::Tensor> decode_paged(
   const at::Tensor k_rows = k_cache.select(0, 0);
   const at::Tensor v_rows = v_cache.select(0, 0);
   ifa4_args a = make_args(q, k_rows, v_rows, rel, cu_q, cu_q, max_q, max_k, rel_extent, causal,
-                          window_left, softmax_scale, 0);
+                          window_left, softmax_scale, flags);
   a.k = k_cache.data_ptr();
   a.v = v_cache.data_ptr();
   a.cu_seqlens_k = nullptr;
@@ -237,7 +237,7 @@ TORCH_LIBRARY(inkling_fa4, m) {
       "decode_paged(Tensor q, Tensor k_cache, Tensor v_cache, Tensor rel_logits, "
       "Tensor cu_seqlens_q, Tensor seqused_k, Tensor block_table, int max_seqlen_q, "
       "int max_seqlen_k, int rel_extent, bool causal, int window_left, float softmax_scale, "
-      "bool return_lse) -> (Tensor, Tensor)");
+      "bool return_lse, int flags) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(inkling_fa4, CUDA, m) {

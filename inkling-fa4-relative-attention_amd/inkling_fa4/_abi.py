@@ -22,6 +22,7 @@ IFA4_FP16 = 1
 IFA4_FP32 = 2
 
 IFA4_FLAG_NO_PRUNE = 0x1
+IFA4_FLAG_BOTTOM_RIGHT = 0x2
 
 # Every function include/ifa4.h declares: name -> (restype, argtypes).
 _c_int32 = ctypes.c_int32
@@ -141,12 +142,13 @@ def prefill_tile(head_dim):
 
 
 def count_tiles(cu_q, cu_k, n_heads, block_args=None, causal=True, window_left=-1,
-                no_prune=False, head_dim=128):
+                no_prune=False, head_dim=128, bottom_right=False):
     """KV tiles the prefill kernel visits vs an unpruned kernel (host count)."""
     batch = len(cu_q) - 1
+    flags = (IFA4_FLAG_NO_PRUNE if no_prune else 0) | \
+        (IFA4_FLAG_BOTTOM_RIGHT if bottom_right else 0)
     a = make_args(batch=batch, n_heads=n_heads, kv_heads=1, head_dim=head_dim,
-                  causal=int(causal), window_left=window_left,
-                  flags=IFA4_FLAG_NO_PRUNE if no_prune else 0)
+                  causal=int(causal), window_left=window_left, flags=flags)
     cq = (ctypes.c_int32 * len(cu_q))(*[int(x) for x in cu_q])
     ck = (ctypes.c_int32 * len(cu_k))(*[int(x) for x in cu_k])
     vis, tot = ctypes.c_int64(), ctypes.c_int64()

@@ -55,6 +55,13 @@ def _resolve(q, k, n_heads, kv_heads, head_dim, softmax_scale):
     return scale
 
 
+_FLAG_BOTTOM_RIGHT = 0x2  # IFA4_FLAG_BOTTOM_RIGHT
+
+
+def _flag_bits(bottom_right, extra=0):
+    return int(extra) | (_FLAG_BOTTOM_RIGHT if bottom_right else 0)
+
+
 def _window_left(window_size):
     if window_size is None:
         return -1
@@ -67,18 +74,22 @@ def inkling_fa4_rel_attention(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
                               max_seqlen_q, max_seqlen_k, rel_extent, causal=True,
                               window_size=(-1, -1), n_heads=None, kv_heads=None,
                               head_dim=None, arch=None, *, softmax_scale=None,
-                              return_lse=False, _flags=0):
+                              return_lse=False, bottom_right=False, _flags=0):
     """Varlen / GQA / chunked / sliding-window prefill forward.
 
     q [total_q, Hq, D], k/v [total_k, Hkv, D] (bf16 or fp16, last dim contiguous),
     rel_logits [total_q, Hq, R' >= rel_extent] (bf16/fp16/fp32, any token stride
     including 0), cu_seqlens_q/k int32 [batch+1] on the same GPU.
     Returns out [total_q, Hq, D] in q.dtype, or (out, lse) with return_lse.
+    bottom_right=True: upstream flash-attn alignment (query i at key position
+    i + Lk - Lq for the bias distance, causal mask and window); the default is
+    the reference's top-left alignment.
     """
     scale = _resolve(q, k, n_heads, kv_heads, head_dim, softmax_scale)
     out, lse = _ops().fwd(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
                           int(max_seqlen_k), int(rel_extent), bool(causal),
-                          _window_left(window_size), scale, bool(return_lse), int(_flags))
+                          _window_left(window_size), scale, bool(return_lse),
+                          _flag_bits(bottom_right, _flags))
     return (out, lse) if return_lse else out
 
 
@@ -87,7 +98,7 @@ def inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqle
                                      max_seqlen_q, max_seqlen_k, rel_extent, causal=True,
                                      window_size=(-1, -1), n_heads=None, kv_heads=None,
                                      head_dim=None, arch=None, *, softmax_scale=None,
-                                     return_lse=False):
+                                     return_lse=False, bottom_right=False):
     """Decode forward: exactly one query token per sequence
     (cu_seqlens_q == arange(batch + 1)), KV split across workgroups and merged
     by log-sum-exp.  Falls through to the prefill kernel when q holds more
@@ -99,10 +110,11 @@ def inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqle
         return inkling_fa4_rel_attention(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
                                          max_seqlen_q, max_seqlen_k, rel_extent, causal,
                                          window_size, softmax_scale=scale,
-                                         return_lse=return_lse)
+                                         return_lse=return_lse, bottom_right=bottom_right)
     out, lse = _ops().decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
                              int(max_seqlen_q), int(max_seqlen_k), int(rel_extent), bool(causal),
-                             _window_left(window_size), scale, bool(return_lse), 0)
+                             _window_left(window_size), scale, bool(return_lse),
+                             _flag_bits(bottom_right))
     return (out, lse) if return_lse else out
 
 
@@ -110,7 +122,8 @@ def inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqle
 def inkling_fa4_rel_attention_decode_paged(q, k_cache, v_cache, rel_logits, cu_seqlens_q,
                                            seqused_k, block_table, max_seqlen_q, max_seqlen_k,
                                            rel_extent, causal=True, window_size=(-1, -1), *,
-                                           softmax_scale=None, return_lse=False):
+                                           softmax_scale=None, return_lse=False,
+                                           bottom_right=False):
     """Decode over a paged KV cache (the serving backend's format,
     outputs/architecture.md:117-120: blocks of 16 tokens).
 
@@ -128,7 +141,7 @@ def inkling_fa4_rel_attention_decode_paged(q, k_cache, v_cache, rel_logits, cu_s
     out, lse = _ops().decode_paged(q, k_cache, v_cache, rel_logits, cu_seqlens_q, seqused_k,
                                    block_table, int(max_seqlen_q), int(max_seqlen_k),
                                    int(rel_extent), bool(causal), _window_left(window_size),
-                                   scale, bool(return_lse))
+                                   scale, bool(return_lse), _flag_bits(bottom_right))
     return (out, lse) if return_lse else out
 
 
@@ -165,13 +178,14 @@ def inkling_fa4_rel_attention_decode_triton(q, k, v, rel_logits, cu_seqlens_q, c
 
 
 def prefill_tile_counts(cu_seqlens_q, cu_seqlens_k, n_heads, causal=True, window_size=(-1, -1),
-                        head_dim=128):
+                        head_dim=128, bottom_right=False):
     """(visited, total) KV tiles of a prefill call: tiles the kernel loads after
     causal/window pruning vs tiles an unpruned kernel would load."""
     cq = [int(x) for x in torch.as_tensor(cu_seqlens_q).cpu().tolist()]
     ck = [int(x) for x in torch.as_tensor(cu_seqlens_k).cpu().tolist()]
     return _abi.count_tiles(cq, ck, n_heads, causal=causal,
-                            window_left=_window_left(window_size), head_dim=head_dim)
+                            window_left=_window_left(window_size), head_dim=head_dim,
+                            bottom_right=bottom_right)
 
 
 def default_scale(head_dim):

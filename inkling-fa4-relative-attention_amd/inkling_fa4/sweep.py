@@ -76,10 +76,15 @@ def cmd_build(args):
 
 
 def _case(workload, seq):
+    import torch
     from inkling_fa4 import testing
 
     if workload == "prefill":
-        return testing.ragged_varlen(), testing.long_prefill(seq, batch=8)
+        # check case: ragged tails, diagonal and bias-band tiles, and a run of
+        # interior tiles (the 700-token sequence)
+        check = testing.make_case("sweep_check", [700, 64, 33], [700, 64, 33], 8, 2, 128,
+                                  torch.bfloat16, seed=2)
+        return check, testing.long_prefill(seq, batch=8)
     return testing.decode(batch=8, seed=21, causal=False), testing.decode(causal=False)
 
 

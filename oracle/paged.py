@@ -44,8 +44,10 @@ def gather_paged(k_cache, v_cache, block_table, seqused_k):
 
 @torch.no_grad()
 def ref_rel_attn_paged_with_lse(q, k_cache, v_cache, rel_logits, cu_seqlens_q, seqused_k,
-                                block_table, scale, rel_extent, causal=True, window_left=None):
+                                block_table, scale, rel_extent, causal=True, window_left=None,
+                                bottom_right=False):
     """Oracle over a paged cache: (out [Tq,Hq,D] in q.dtype, lse [Hq,Tq] fp32)."""
     k, v, cu_k = gather_paged(k_cache, v_cache, block_table, seqused_k)
     return ref_rel_attn_with_lse(q, k, v, rel_logits, cu_seqlens_q, cu_k, scale, rel_extent,
-                                 causal=causal, window_left=window_left)
+                                 causal=causal, window_left=window_left,
+                                 bottom_right=bottom_right)

@@ -32,8 +32,15 @@ def _lengths(cu):
 
 @torch.no_grad()
 def ref_rel_attn_with_lse(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k, scale,
-                          rel_extent, causal=True, window_left=None):
-    """Return (out [Tq,Hq,D] in q.dtype, lse [Hq,Tq] fp32)."""
+                          rel_extent, causal=True, window_left=None, bottom_right=False):
+    """Return (out [Tq,Hq,D] in q.dtype, lse [Hq,Tq] fp32).
+
+    bottom_right=True is an addition with no counterpart in the reference: the
+    upstream flash-attn alignment of its serving backend
+    (outputs/architecture.md:72, d = (i + sk - sq) - j).  Query i sits at key
+    position i + (Lk - Lq) for the bias distance, the causal mask and the
+    window.  It equals the reference semantics when Lq == Lk.
+    """
     n_q, hq, _ = q.shape
     hkv = k.shape[1]
     if hq % hkv:
@@ -47,14 +54,19 @@ def ref_rel_attn_with_lse(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k, scale
             continue
         rows = torch.arange(lq, device=q.device).unsqueeze(1)
         cols = torch.arange(lk, device=q.device).unsqueeze(0)
-        dist = rows - cols + (lq - lk)
+        if bottom_right:
+            pos = rows + (lk - lq)          # key position of query i
+            dist = pos - cols
+        else:
+            pos = rows                      # reference.py:36-37 (top-left)
+            dist = rows - cols + (lq - lk)  # reference.py:28-31
         band = (dist >= 0) & (dist < rel_extent)
         gather_idx = dist.clamp(min=0, max=rel_extent - 1)
         visible = torch.ones(lq, lk, dtype=torch.bool, device=q.device)
         if causal:
-            visible &= rows >= cols
+            visible &= pos >= cols
         if window_left is not None:
-            visible &= (rows - cols) <= window_left
+            visible &= (pos - cols) <= window_left
         for h in range(hq):
             kh = h // group
             qf = q[q0:q1, h].float()

@@ -152,12 +152,12 @@ def test_tile_table_view():
     assert autotune_configs._detect_arch().startswith("gfx")
 
 
-def _needed_tiles(lens_q, lens_k, causal, window, bq, bk):
+def _needed_tiles(lens_q, lens_k, causal, window, bq, bk, bottom_right=False):
     """KV tiles holding at least one visible pair, per query tile (brute force
-    over the visibility mask of the reference semantics)."""
+    over the visibility mask; bottom_right: query i at key position i + lk - lq)."""
     n = 0
     for lq, lk in zip(lens_q, lens_k):
-        i = torch.arange(lq).unsqueeze(1)
+        i = torch.arange(lq).unsqueeze(1) + ((lk - lq) if bottom_right else 0)
         j = torch.arange(lk).unsqueeze(0)
         vis = torch.ones(lq, lk, dtype=torch.bool)
         if causal:
@@ -254,3 +254,23 @@ def test_paged_workspace_equals_contiguous_workspace():
     assert lib.ifa4_decode_workspace_bytes(ctypes.byref(a)) == 0
     assert lib.ifa4_decode_paged_fwd(ctypes.byref(a), None, 256, 1 << 30, None) == \
         _abi.IFA4_EINVAL
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_pruning_bottom_right_visits_exactly_the_tiles_with_visible_pairs(seed):
+    """Bottom-right alignment, with Lq below and above Lk."""
+    g = torch.Generator().manual_seed(100 + seed)
+    batch = 3
+    lens_q = torch.randint(1, 400, (batch,), generator=g).tolist()
+    lens_k = [max(1, a + b) for a, b in
+              zip(lens_q, torch.randint(-150, 300, (batch,), generator=g).tolist())]
+    window = [-1, 63, 5, 200, -1, 0][seed]
+    causal = seed != 4
+    cu_q = [0] + list(torch.tensor(lens_q).cumsum(0).tolist())
+    cu_k = [0] + list(torch.tensor(lens_k).cumsum(0).tolist())
+    t = _abi.prefill_tile(128)
+    visited, total = _abi.count_tiles(cu_q, cu_k, 1, causal=causal, window_left=window,
+                                      bottom_right=True)
+    need = _needed_tiles(lens_q, lens_k, causal, window, t.block_q, t.block_k,
+                         bottom_right=True)
+    assert visited == need
