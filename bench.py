@@ -9,7 +9,8 @@ with the reference's own 2*S^2*D*Hq*B count alongside.
 Also measured in the same run: split-KV decode (batch 64, one query per
 sequence, KV lengths U[1024,16384] seeded, non-causal so the whole cache is
 streamed) as KV GB/s against the 8 TB/s HBM peak, also with the same keys in
-a paged cache (blocks of 16 tokens, shuffled); the other prefill sequence
+a paged cache (blocks of 16 tokens, shuffled) and as an fp8 (e4m3) cache; the
+other prefill sequence
 lengths {1024, 2048, 8192}; and, as the CPU baseline, the fp32 CPU oracle over
 the whole headline batch (median of up to 3 passes, at most ~30 s).
 
@@ -125,9 +126,10 @@ def prefill_bench(seq_len, steps, warmup, batch=8):
     }, case
 
 
-def decode_bench(steps, warmup, block_size=0):
+def decode_bench(steps, warmup, block_size=0, fp8=False):
     """Decode over the 64-sequence batch; block_size > 0: the same keys in a
-    paged cache of that block size (blocks in a shuffled physical order)."""
+    paged cache of that block size (blocks in a shuffled physical order);
+    fp8: the keys and values stored as float8_e4m3fn with per-tensor scales."""
     import torch
     from inkling_fa4 import (inkling_fa4_rel_attention_decode,
                              inkling_fa4_rel_attention_decode_paged, testing)
@@ -136,13 +138,21 @@ def decode_bench(steps, warmup, block_size=0):
     lens_k = (case.cu_k[1:] - case.cu_k[:-1])
     sum_l = int(lens_k.sum())
     hkv, d = case.k.shape[1], case.k.shape[2]
-    esize = case.k.element_size()
+    esize = 1 if fp8 else case.k.element_size()
     kv_bytes = sum_l * hkv * d * 2 * esize
-    qo_bytes = 2 * case.q.numel() * esize
+    qo_bytes = 2 * case.q.numel() * case.q.element_size()
     table_bytes = 0
     c = case.to("cuda")
     args = c.args()
-    if block_size:
+    if fp8:
+        k8, v8, ks, vs, _ = testing.fp8_kv(case)
+        k8, v8 = k8.to("cuda"), v8.to("cuda")
+
+        def step():
+            return inkling_fa4_rel_attention_decode(
+                c.q, k8, v8, c.rel, c.cu_q, c.cu_k, c.max_q, c.max_k, c.rel_extent,
+                causal=False, softmax_scale=c.scale, k_scale=ks, v_scale=vs)
+    elif block_size:
         pk = testing.paginate(case, block_size=block_size, seed=0, spare_blocks=0,
                               fill=0.0).to("cuda")
         table_bytes = 4 * int(((lens_k + block_size - 1) // block_size).sum())
@@ -162,6 +172,8 @@ def decode_bench(steps, warmup, block_size=0):
            "us": ms * 1e3, "gbps": gbps, "frac_of_peak": gbps / HBM_PEAK_GBPS}
     if block_size:
         out["block_size"] = block_size
+    if fp8:
+        out["kv_dtype"] = "float8_e4m3fn"
     return out
 
 
@@ -363,6 +375,11 @@ def main():
         log(f"decode paged: {dp['us']:.1f} us  {dp['gbps']:.0f} GB/s")
         result["decode_paged"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                   for k, v in dp.items()}
+        log(f"decode, fp8 KV cache: {args.steps} steps")
+        d8 = decode_bench(args.steps, args.warmup, fp8=True)
+        log(f"decode fp8: {d8['us']:.1f} us  {d8['gbps']:.0f} GB/s")
+        result["decode_fp8"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                for k, v in d8.items()}
         if result["value"] is None:
             result["value"] = round(dec["gbps"], 1)
             result["unit"] = "GB/s"

@@ -43,7 +43,8 @@ typedef enum ifa4_status {
 typedef enum ifa4_dtype {
   IFA4_BF16 = 0,
   IFA4_FP16 = 1,
-  IFA4_FP32 = 2
+  IFA4_FP32 = 2,
+  IFA4_FP8_E4M3 = 3   /* OCP e4m3 (float8_e4m3fn); K/V of ifa4_decode_quant_fwd only */
 } ifa4_dtype;
 
 /* Flags (ifa4_args.flags). */
@@ -200,6 +201,29 @@ typedef struct ifa4_paged_kv {
  */
 size_t ifa4_decode_paged_workspace_bytes(const ifa4_args* args, const ifa4_paged_kv* kv);
 int32_t ifa4_decode_paged_fwd(const ifa4_args* args, const ifa4_paged_kv* kv, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/*
+ * Quantised KV cache for decode: K and V stored as fp8 (OCP e4m3), one scale
+ * per tensor (k = k_stored * k_scale, v = v_stored * v_scale), the serving
+ * backend's FP8 KV cache (outputs/architecture.md:127, "Dtype: BF16 / FP8").
+ * q, out and rel keep args.qkv_dtype / rel_dtype; K/V strides are in fp8
+ * elements (bytes) and must be multiples of 16.  It halves the bytes decode
+ * streams.  The result is that of ifa4_decode_fwd on the dequantised K/V
+ * (computed in fp32 from the exact fp8 values).
+ */
+typedef struct ifa4_kv_quant {
+  uint32_t struct_size;   /* sizeof(ifa4_kv_quant) */
+  int32_t kv_dtype;       /* IFA4_FP8_E4M3 */
+  float k_scale;          /* > 0, finite */
+  float v_scale;          /* > 0, finite */
+} ifa4_kv_quant;
+
+/* kv: NULL for contiguous K/V (args.cu_seqlens_k), else a paged cache. */
+size_t ifa4_decode_quant_workspace_bytes(const ifa4_args* args, const ifa4_paged_kv* kv,
+                                         const ifa4_kv_quant* quant);
+int32_t ifa4_decode_quant_fwd(const ifa4_args* args, const ifa4_paged_kv* kv,
+                              const ifa4_kv_quant* quant, void* workspace,
                               size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus

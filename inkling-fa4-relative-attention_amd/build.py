@@ -45,18 +45,20 @@ def _run(cmd):
         print(out)
 
 
-def build_library(jobs, out_dir=PKG, defines=(), build_dir=BUILD):
+def build_library(jobs, out_dir=PKG, defines=(), build_dir=BUILD, csrc=CSRC, include=INCLUDE):
     """Compile the kernels and the C ABI into out_dir/libifa4.so.  `defines`:
-    extra -D flags (tile-sweep knobs of the kernel sources)."""
+    extra -D flags (tile-sweep knobs of the kernel sources); `csrc` / `include`:
+    source directories (a sweep builds every variant from one snapshot)."""
     os.makedirs(build_dir, exist_ok=True)
-    flags = HIP_FLAGS + [f"-D{d}" for d in defines]
+    flags = [f for f in HIP_FLAGS if not f.startswith("-I")] + [f"-I{include}", f"-I{csrc}"]
+    flags += [f"-D{d}" for d in defines]
     objs = []
     cmds = []
     for src in LIB_SOURCES:
         obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        cmds.append([HIPCC] + flags + lang + ["-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC] + flags + lang + ["-c", os.path.join(csrc, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
     os.makedirs(out_dir, exist_ok=True)

@@ -44,19 +44,34 @@ namespace ifa4 {
 namespace {
 
 constexpr int kStep = 32;  // keys per pipeline step of a decode wave
+constexpr int kDecodeFp8MaxGroup = 8;
 
-// Lane layouts of a decode wave (D = head_dim):
-//   row layout (loads, PV):  r = lane / (D/8) is the row within a wave load,
-//                            c = lane % (D/8) the 16-byte d chunk;
+// Lane layouts of a decode wave (D = head_dim, Eb = bytes per K/V element):
+//   row layout (loads, PV):  r = lane / kLpr is the row within a wave load,
+//                            c = lane % kLpr the 16-byte chunk (16/Eb elements);
 //   S^T layout (QK):         n = lane % 16 the query head, g = lane / 16.
-template <int D>
+template <int D, int Eb>
 struct DecodeShape {
-  static constexpr int kLpr = D / 8;           // lanes per K/V row
+  static constexpr int kLpr = D * Eb / 16;     // lanes per K/V row
+  static constexpr int kEpl = 16 / Eb;         // elements of a row per lane
   static constexpr int kRpi = 64 / kLpr;       // rows per wave load
   static constexpr int kLoads = kStep / kRpi;  // wave loads per tensor per step
+  static constexpr int kGroupRows = kRpi > 8 ? kRpi : 8;  // paged: rows per resource
   static constexpr int kPitch = D + 8;         // LDS K row pitch (elements)
   static constexpr int kKSteps = D / 32;       // 16x16x32 MFMAs per 16 keys
 };
+
+// 8 fp8 (OCP e4m3) values in two dwords (byte i = element i) -> fp32, exactly;
+// every e4m3 value is also exact in bf16 and fp16.
+__device__ __forceinline__ void fp8x8_to_f32(uint32_t w0, uint32_t w1, float* f) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w0, false);
+  const f32x2_t b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w0, true);
+  const f32x2_t c = __builtin_amdgcn_cvt_pk_f32_fp8((int)w1, false);
+  const f32x2_t d = __builtin_amdgcn_cvt_pk_f32_fp8((int)w1, true);
+  f[0] = a[0]; f[1] = a[1]; f[2] = b[0]; f[3] = b[1];
+  f[4] = c[0]; f[5] = c[1]; f[6] = d[0]; f[7] = d[1];
+}
 
 // One Q slot in LDS: the G heads of a kv head, [G][D], in whole 1 KiB DMAs.
 template <int D, int G>
@@ -161,10 +176,10 @@ __device__ __forceinline__ int step_key0(const Cursor& cu) {
   return (cu.kbeg & ~(kStep - 1)) + cu.step * kStep;
 }
 
-template <int D, typename Tag, int G, bool kPaged>
+template <int D, typename Tag, int G, bool kPaged, int Eb>
 __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
   using E = Elem<Tag>;
-  using S = DecodeShape<D>;
+  using S = DecodeShape<D, Eb>;
 
   __shared__ __align__(16) uint16_t k_lds[kStep * S::kPitch];
   using Q = DecodeQ<D, G>;
@@ -230,11 +245,14 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
   };
 
   // ---- loads of one step, Q of a segment ---------------------------------------------
-  const uint32_t k_row = (uint32_t)p.k_st * 2, v_row = (uint32_t)p.v_st * 2;
+  const uint32_t k_row = (uint32_t)p.k_st * Eb, v_row = (uint32_t)p.v_st * Eb;
+  const char* const k_bytes0 = static_cast<const char*>(p.k);
+  const char* const v_bytes0 = static_cast<const char*>(p.v);
   // Paged cache: lane L holds table entry tw_base + L of sequence tw_seq (a
   // window of 64 blocks; a 32-key step never straddles two windows).  A step
-  // reads its 8-key row groups through one buffer resource per block, so rows
-  // past the sequence end and entries outside the pool read as zero.
+  // reads its row groups (8 keys, or the rows of one wave load when larger)
+  // through one buffer resource per block, so rows past the sequence end and
+  // entries outside the pool read as zero.
   int tw = -1, tw_seq = -1, tw_base = 0;
   const int bmask = (1 << p.block_shift) - 1;
   auto load_paged = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu) {
@@ -247,20 +265,19 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
       const int e = tw_base + lane;
       tw = e < nblk ? p.block_table[(int64_t)cu.seq * p.bt_stride + e] : -1;
     }
-    const uint32_t k_bytes = (uint32_t)(((int64_t)bmask * p.k_st + D) * 2);
-    const uint32_t v_bytes = (uint32_t)(((int64_t)bmask * p.v_st + D) * 2);
-    constexpr int kGroups = kStep / 8;
+    const uint32_t k_bytes = (uint32_t)(((int64_t)bmask * p.k_st + D) * Eb);
+    const uint32_t v_bytes = (uint32_t)(((int64_t)bmask * p.v_st + D) * Eb);
+    constexpr int kGroups = kStep / S::kGroupRows;
     rsrc_t rk[kGroups], rv[kGroups];
 #pragma unroll
     for (int grp = 0; grp < kGroups; ++grp) {
-      const int ent = __builtin_amdgcn_readlane(tw, ((k0 + 8 * grp) >> p.block_shift) - tw_base);
+      const int ent = __builtin_amdgcn_readlane(
+          tw, ((k0 + S::kGroupRows * grp) >> p.block_shift) - tw_base);
       const bool ok = (unsigned)ent < (unsigned)p.num_blocks;
       const int64_t eb = ok ? (int64_t)ent : 0;
-      rk[grp] = make_rsrc_uniform(static_cast<const uint16_t*>(p.k) + eb * p.k_sblk +
-                                      (int64_t)cu.kvh * p.k_sh,
+      rk[grp] = make_rsrc_uniform(k_bytes0 + (eb * p.k_sblk + (int64_t)cu.kvh * p.k_sh) * Eb,
                                   ok ? k_bytes : 0u);
-      rv[grp] = make_rsrc_uniform(static_cast<const uint16_t*>(p.v) + eb * p.v_sblk +
-                                      (int64_t)cu.kvh * p.v_sh,
+      rv[grp] = make_rsrc_uniform(v_bytes0 + (eb * p.v_sblk + (int64_t)cu.kvh * p.v_sh) * Eb,
                                   ok ? v_bytes : 0u);
     }
 #pragma unroll
@@ -268,22 +285,21 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
       const int key = k0 + S::kRpi * i + r;
       const uint32_t row = (uint32_t)(key & bmask);
       const bool valid = key < cu.kend;
-      kr[i] = buf_load_16(rk[(S::kRpi * i) / 8], valid ? row * k_row + 16 * c : kOutOfRange);
-      vr[i] = buf_load_16(rv[(S::kRpi * i) / 8], valid ? row * v_row + 16 * c : kOutOfRange);
+      const int grp = (S::kRpi * i) / S::kGroupRows;
+      kr[i] = buf_load_16(rk[grp], valid ? row * k_row + 16 * c : kOutOfRange);
+      vr[i] = buf_load_16(rv[grp], valid ? row * v_row + 16 * c : kOutOfRange);
     }
   };
   auto load = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu) {
     if constexpr (kPaged) {
       load_paged(kr, vr, cu);
     } else {
-      const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + (int64_t)cu.ks * p.k_st +
-                              (int64_t)cu.kvh * p.k_sh;
-      const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + (int64_t)cu.ks * p.v_st +
-                              (int64_t)cu.kvh * p.v_sh;
+      const char* kbase = k_bytes0 + ((int64_t)cu.ks * p.k_st + (int64_t)cu.kvh * p.k_sh) * Eb;
+      const char* vbase = v_bytes0 + ((int64_t)cu.ks * p.v_st + (int64_t)cu.kvh * p.v_sh) * Eb;
       const rsrc_t rk =
-          make_rsrc_uniform(kbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.k_st + D) * 2));
+          make_rsrc_uniform(kbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.k_st + D) * Eb));
       const rsrc_t rv =
-          make_rsrc_uniform(vbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.v_st + D) * 2));
+          make_rsrc_uniform(vbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.v_st + D) * Eb));
       const int k0 = step_key0(cu);
 #pragma unroll
       for (int i = 0; i < S::kLoads; ++i) {
@@ -313,7 +329,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
   const float c2 = p.scale_log2;
   float m_run = -INFINITY;  // per head n (S^T lanes), identical over g
   float l_run = 0.f;        // partial sum over this lane's keys
-  float o[G][8];
+  float o[G][S::kEpl];
   u32x4_t qf[S::kKSteps];
 
   auto step = [&](const u32x4_t* kr, const u32x4_t* vr, const Cursor& cu, bool last) {
@@ -323,7 +339,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
 #pragma unroll
       for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+        for (int e = 0; e < S::kEpl; ++e) o[h][e] = 0.f;
       if (cu.step == 0 && lane == 0) {
         // this wave holds the segment's first step: record the covering waves
         p.ws_meta[2 * cu.seg] = w;
@@ -333,8 +349,22 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
     // K rows -> LDS (row-major, padded rows: conflict-free A-operand reads).
     // Waiting for these loads also completes the (earlier) Q DMA of the segment.
 #pragma unroll
-    for (int i = 0; i < S::kLoads; ++i)
-      *reinterpret_cast<u32x4_t*>(k_lds + (S::kRpi * i + r) * S::kPitch + 8 * c) = kr[i];
+    for (int i = 0; i < S::kLoads; ++i) {
+      uint16_t* dst = k_lds + (S::kRpi * i + r) * S::kPitch + S::kEpl * c;
+      if constexpr (Eb == 2) {
+        *reinterpret_cast<u32x4_t*>(dst) = kr[i];
+      } else {
+        // fp8 -> the MFMA type (exact); the K scale is folded into the logit scale
+#pragma unroll
+        for (int hlf = 0; hlf < 2; ++hlf) {
+          float f[8];
+          fp8x8_to_f32(kr[i][2 * hlf], kr[i][2 * hlf + 1], f);
+          *reinterpret_cast<u32x4_t*>(dst + 8 * hlf) =
+              u32x4_t{E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]),
+                      E::pack2(f[6], f[7])};
+        }
+      }
+    }
     wave_lds_sync();
     if (cu.first) {
       // Q (B operand): column n = head n of the kv head, k-slots = d 32*kk + 8*g .. +7.
@@ -420,17 +450,22 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
       const int kl = S::kRpi * i + r;
-      float vv[8];
+      float vv[S::kEpl];
+      if constexpr (Eb == 2) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        vv[2 * q] = E::lo(vr[i][q]);
-        vv[2 * q + 1] = E::hi(vr[i][q]);
+        for (int q = 0; q < 4; ++q) {
+          vv[2 * q] = E::lo(vr[i][q]);
+          vv[2 * q + 1] = E::hi(vr[i][q]);
+        }
+      } else {
+        fp8x8_to_f32(vr[i][0], vr[i][1], vv);
+        fp8x8_to_f32(vr[i][2], vr[i][3], vv + 8);
       }
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         const float ph = p_lds[kl * G + h];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] = fmaf(ph, vv[e], o[h][e]);
+        for (int e = 0; e < S::kEpl; ++e) o[h][e] = fmaf(ph, vv[e], o[h][e]);
       }
     }
     wave_lds_sync();  // p_lds is rewritten by the next step
@@ -441,11 +476,11 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < S::kEpl; ++e) {
         float v = o[h][e];
 #pragma unroll
         for (int off = S::kLpr; off < 64; off <<= 1) {
-          if (off == 8) v += __shfl_xor(v, 8);
+          if (off < 16) v += __shfl_xor(v, off);
           else if (off == 16) v = add_xor16(v);
           else v = add_xor32(v);
         }
@@ -457,12 +492,13 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
       for (int h = 0; h < G; ++h) {
         if (h < g_act) {
           const float lt = readlane_f(l_tot, h);
-          const float inv = lt > 0.f ? 1.f / lt : 0.f;
-          float* dst = p.ws_o + ((int64_t)slot * g_act + h) * D + 8 * c;
-          *reinterpret_cast<f32x4_t*>(dst) = f32x4_t{o[h][0] * inv, o[h][1] * inv, o[h][2] * inv,
-                                                     o[h][3] * inv};
-          *reinterpret_cast<f32x4_t*>(dst + 4) = f32x4_t{o[h][4] * inv, o[h][5] * inv,
-                                                         o[h][6] * inv, o[h][7] * inv};
+          const float inv = lt > 0.f ? p.v_scale / lt : 0.f;  // V scale (1 for 16-bit V)
+          float* dst = p.ws_o + ((int64_t)slot * g_act + h) * D + S::kEpl * c;
+#pragma unroll
+          for (int q = 0; q < S::kEpl / 4; ++q)
+            *reinterpret_cast<f32x4_t*>(dst + 4 * q) =
+                f32x4_t{o[h][4 * q] * inv, o[h][4 * q + 1] * inv, o[h][4 * q + 2] * inv,
+                        o[h][4 * q + 3] * inv};
         }
       }
     }
@@ -614,12 +650,25 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
 template <int D, typename Tag, int G>
 hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   if (p.n_waves > 0) {
-    if (p.block_table != nullptr)
-      hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true>), dim3(p.n_waves), dim3(64), 0,
-                         stream, p);
-    else
-      hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false>), dim3(p.n_waves), dim3(64), 0,
-                         stream, p);
+    const dim3 grid(p.n_waves), block(64);
+    if (p.kv_fp8) {
+      // fp8 K/V: 16 elements per lane, so o[G][16]; up to G = 8 fits in registers
+      if constexpr (G <= kDecodeFp8MaxGroup) {
+        if (p.block_table != nullptr)
+          hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 1>), grid, block, 0, stream,
+                             p);
+        else
+          hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 1>), grid, block, 0, stream,
+                             p);
+      } else {
+        return hipErrorInvalidValue;  // rejected on the host before any launch
+      }
+    } else {
+      if (p.block_table != nullptr)
+        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 2>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 2>), grid, block, 0, stream, p);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -640,6 +689,7 @@ hipError_t launch_decode_d(const DecodeParams& p, hipStream_t stream) {
 }  // namespace
 
 int decode_max_group() { return 16; }
+int decode_fp8_max_group() { return kDecodeFp8MaxGroup; }
 
 hipError_t launch_decode(const DecodeParams& p, int head_dim, int qkv_dtype, hipStream_t stream) {
   if (p.batch <= 0) return hipSuccess;

@@ -23,7 +23,8 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 
 // kv != nullptr: K/V are a paged cache described by *kv (checked by
 // check_paged); cu_seqlens_k is then not read and may be NULL.
-int32_t check_args(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr) {
+// kv_esize: bytes per K/V element (2, or 1 for an fp8 cache).
+int32_t check_args(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr, int kv_esize = 2) {
   if (a == nullptr) return IFA4_EINVAL;
   if (a->struct_size != sizeof(ifa4_args)) return IFA4_EINVAL;
   if (a->batch < 0 || a->n_heads < 1 || a->kv_heads < 1) return IFA4_EINVAL;
@@ -57,8 +58,9 @@ int32_t check_args(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr) {
   // 16-byte vector loads of q/k/v rows, 8-byte stores of out rows.
   if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->out, 16))
     return IFA4_EUNSUPPORTED;
-  if ((a->q_stride_t | a->q_stride_h | a->k_stride_t | a->k_stride_h | a->v_stride_t |
-       a->v_stride_h | a->out_stride_t | a->out_stride_h) % 8 != 0)
+  if ((a->q_stride_t | a->q_stride_h | a->out_stride_t | a->out_stride_h) % 8 != 0)
+    return IFA4_EUNSUPPORTED;
+  if ((a->k_stride_t | a->k_stride_h | a->v_stride_t | a->v_stride_h) % (16 / kv_esize) != 0)
     return IFA4_EUNSUPPORTED;
   if (a->rel != nullptr && !aligned(a->rel, a->rel_dtype == IFA4_FP32 ? 4 : 2))
     return IFA4_EINVAL;
@@ -75,17 +77,19 @@ int32_t check_args(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr) {
   // a paged cache is addressed one block at a time (check_paged)
   const int64_t k_rows = kv == nullptr ? a->max_seqlen_k + kpad : 0;
   if ((a->max_seqlen_q + kpad) * a->q_stride_t * 2 >= kLimit ||
-      k_rows * a->k_stride_t * 2 >= kLimit || k_rows * a->v_stride_t * 2 >= kLimit ||
+      k_rows * a->k_stride_t * kv_esize >= kLimit || k_rows * a->v_stride_t * kv_esize >= kLimit ||
       ((a->max_seqlen_q + kpad) * a->rel_stride_t + a->rel_width) * rel_esize >= kLimit)
     return IFA4_EUNSUPPORTED;
   return IFA4_OK;
 }
 
 // Paged KV cache description (include/ifa4.h, ifa4_paged_kv).
-int32_t check_paged(const ifa4_args* a, const ifa4_paged_kv* kv) {
+int32_t check_paged(const ifa4_args* a, const ifa4_paged_kv* kv, int kv_esize = 2) {
   if (kv == nullptr || kv->struct_size != sizeof(ifa4_paged_kv)) return IFA4_EINVAL;
   const int32_t bs = kv->block_size;
   if (bs < 8 || bs > 65536 || (bs & (bs - 1)) != 0) return IFA4_EINVAL;
+  // one wave load covers 1024 / (head_dim * esize) rows, all within one block
+  if (a->head_dim > 0 && bs < 1024 / (a->head_dim * kv_esize)) return IFA4_EUNSUPPORTED;
   if (kv->block_table_stride < 0 || kv->k_stride_block < 0 || kv->v_stride_block < 0 ||
       kv->num_blocks < 0 || kv->max_blocks_per_seq < 0)
     return IFA4_EINVAL;
@@ -98,10 +102,10 @@ int32_t check_paged(const ifa4_args* a, const ifa4_paged_kv* kv) {
   if ((int64_t)kv->max_blocks_per_seq * bs < a->max_seqlen_k) return IFA4_EINVAL;
   if ((int64_t)kv->max_blocks_per_seq * bs > (int64_t(1) << 30)) return IFA4_EUNSUPPORTED;
   // 16-byte loads from every block; one block of one kv head spans < 2 GiB
-  if ((kv->k_stride_block | kv->v_stride_block) % 8 != 0) return IFA4_EUNSUPPORTED;
+  if ((kv->k_stride_block | kv->v_stride_block) % (16 / kv_esize) != 0) return IFA4_EUNSUPPORTED;
   const int64_t kLimit = int64_t(1) << 31;
-  if (((int64_t)(bs - 1) * a->k_stride_t + a->head_dim) * 2 >= kLimit ||
-      ((int64_t)(bs - 1) * a->v_stride_t + a->head_dim) * 2 >= kLimit)
+  if (((int64_t)(bs - 1) * a->k_stride_t + a->head_dim) * kv_esize >= kLimit ||
+      ((int64_t)(bs - 1) * a->v_stride_t + a->head_dim) * kv_esize >= kLimit)
     return IFA4_EUNSUPPORTED;
   return IFA4_OK;
 }
@@ -169,18 +173,33 @@ DecodeLayout decode_layout(const ifa4_args* a) {
   return l;
 }
 
-int32_t check_decode(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr) {
-  int32_t st = check_args(a, kv);
-  if (st != IFA4_OK) return st;
-  if (kv != nullptr && (st = check_paged(a, kv)) != IFA4_OK) return st;
+// Quantised K/V description (include/ifa4.h, ifa4_kv_quant).
+int32_t check_quant(const ifa4_kv_quant* qt) {
+  if (qt->struct_size != sizeof(ifa4_kv_quant)) return IFA4_EINVAL;
+  if (qt->kv_dtype != IFA4_FP8_E4M3) return IFA4_EUNSUPPORTED;
+  if (!std::isfinite(qt->k_scale) || !std::isfinite(qt->v_scale) || !(qt->k_scale > 0.f) ||
+      !(qt->v_scale > 0.f))
+    return IFA4_EINVAL;
+  return IFA4_OK;
+}
+
+int32_t check_decode(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr,
+                     const ifa4_kv_quant* qt = nullptr) {
+  int32_t st = IFA4_OK;
+  if (qt != nullptr && (st = check_quant(qt)) != IFA4_OK) return st;
+  const int esize = qt != nullptr ? 1 : 2;
+  if ((st = check_args(a, kv, esize)) != IFA4_OK) return st;
+  if (kv != nullptr && (st = check_paged(a, kv, esize)) != IFA4_OK) return st;
+  if (qt != nullptr && a->n_heads / a->kv_heads > ifa4::decode_fp8_max_group())
+    return IFA4_EUNSUPPORTED;
   if (a->batch > 0 && a->total_q != a->batch) return IFA4_EINVAL;  // one query per sequence
   if (a->n_heads / a->kv_heads > ifa4::decode_max_group()) return IFA4_EUNSUPPORTED;
   return IFA4_OK;
 }
 
-int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, void* workspace,
-                   size_t workspace_bytes, void* stream) {
-  const int32_t st = check_decode(args, kv);
+int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv_quant* qt,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  const int32_t st = check_decode(args, kv, qt);
   if (st != IFA4_OK) return st;
   if (args->batch == 0) return IFA4_OK;
   const DecodeLayout lay = decode_layout(args);
@@ -221,7 +240,9 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, void* workspa
   p.window_left = args->window_left;
   p.rel_dtype = args->rel_dtype;
   p.n_waves = decode_waves(args);
-  p.scale_log2 = args->softmax_scale * kLog2eHost;
+  p.kv_fp8 = qt != nullptr ? 1 : 0;
+  p.scale_log2 = args->softmax_scale * (qt != nullptr ? qt->k_scale : 1.f) * kLog2eHost;
+  p.v_scale = qt != nullptr ? qt->v_scale : 1.f;
   if (kv != nullptr) {
     p.block_table = kv->block_table;
     p.seqused_k = kv->seqused_k;
@@ -342,7 +363,7 @@ int32_t ifa4_decode_tile(const ifa4_args* args, ifa4_tile* tile) {
 
 int32_t ifa4_decode_fwd(const ifa4_args* args, void* workspace, size_t workspace_bytes,
                         void* stream) {
-  return run_decode(args, nullptr, workspace, workspace_bytes, stream);
+  return run_decode(args, nullptr, nullptr, workspace, workspace_bytes, stream);
 }
 
 size_t ifa4_decode_paged_workspace_bytes(const ifa4_args* args, const ifa4_paged_kv* kv) {
@@ -353,7 +374,20 @@ size_t ifa4_decode_paged_workspace_bytes(const ifa4_args* args, const ifa4_paged
 int32_t ifa4_decode_paged_fwd(const ifa4_args* args, const ifa4_paged_kv* kv, void* workspace,
                               size_t workspace_bytes, void* stream) {
   if (kv == nullptr) return IFA4_EINVAL;
-  return run_decode(args, kv, workspace, workspace_bytes, stream);
+  return run_decode(args, kv, nullptr, workspace, workspace_bytes, stream);
+}
+
+size_t ifa4_decode_quant_workspace_bytes(const ifa4_args* args, const ifa4_paged_kv* kv,
+                                         const ifa4_kv_quant* quant) {
+  if (quant == nullptr || check_decode(args, kv, quant) != IFA4_OK) return 0;
+  return (size_t)decode_layout(args).total();
+}
+
+int32_t ifa4_decode_quant_fwd(const ifa4_args* args, const ifa4_paged_kv* kv,
+                              const ifa4_kv_quant* quant, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (quant == nullptr) return IFA4_EINVAL;
+  return run_decode(args, kv, quant, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -55,7 +55,9 @@ struct DecodeParams {
   int32_t window_left;   // -1: none (only matters with bottom_right: top-left decode never masks)
   int32_t rel_dtype;
   int32_t n_waves;   // persistent waves of pass 1 (0: nothing to stream)
+  int32_t kv_fp8;    // 1: K and V are fp8 (OCP e4m3), K scale folded into scale_log2
   float scale_log2;
+  float v_scale;     // multiplies the output (1 for 16-bit V)
   // Paged KV cache (block_table != nullptr): k/v are block pools, key j of
   // sequence b is row j & (2^block_shift - 1) of block
   // block_table[b * bt_stride + (j >> block_shift)]; lengths from seqused_k.
@@ -73,6 +75,7 @@ int prefill_waves();
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, int qkv_dtype, hipStream_t stream);
 
 int decode_max_group();
+int decode_fp8_max_group();
 hipError_t launch_decode(const DecodeParams& p, int head_dim, int qkv_dtype, hipStream_t stream);
 
 }  // namespace ifa4

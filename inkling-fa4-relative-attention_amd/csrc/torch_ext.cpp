@@ -49,8 +49,9 @@ ifa4_args make_args(const at::Tensor& q, const at::Tensor& k, const at::Tensor& 
   TORCH_CHECK(q.size(2) == k.size(2), "inkling_fa4: q and k head_dim differ");
   TORCH_CHECK(rel.size(0) == q.size(0) && rel.size(1) == q.size(1),
               "inkling_fa4: rel_logits must be [total_q, n_heads, >= rel_extent]");
-  TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type(),
-              "inkling_fa4: q, k, v dtypes differ");
+  const bool kv_fp8 = k.scalar_type() == at::kFloat8_e4m3fn;
+  TORCH_CHECK(k.scalar_type() == v.scalar_type() && (kv_fp8 || q.scalar_type() == k.scalar_type()),
+              "inkling_fa4: q, k, v dtypes differ (k/v may both be float8_e4m3fn in decode)");
   TORCH_CHECK(q.stride(2) == 1 && k.stride(2) == 1 && v.stride(2) == 1 && rel.stride(2) == 1,
               "inkling_fa4: the last dim of q, k, v, rel_logits must be contiguous");
   TORCH_CHECK(cu_q.scalar_type() == at::kInt && cu_k.scalar_type() == at::kInt,
@@ -100,12 +101,24 @@ ifa4_args make_args(const at::Tensor& q, const at::Tensor& k, const at::Tensor& 
   return a;
 }
 
+// fp8 K/V (decode only): the per-tensor scales as an ifa4_kv_quant.
+ifa4_kv_quant kv_quant(double k_scale, double v_scale) {
+  ifa4_kv_quant qt{};
+  qt.struct_size = sizeof(ifa4_kv_quant);
+  qt.kv_dtype = IFA4_FP8_E4M3;
+  qt.k_scale = static_cast<float>(k_scale);
+  qt.v_scale = static_cast<float>(v_scale);
+  return qt;
+}
+
 std::tuple<at::Tensor, at::Tensor> fwd(const at::Tensor& q, const at::Tensor& k,
                                        const at::Tensor& v, const at::Tensor& rel,
                                        const at::Tensor& cu_q, const at::Tensor& cu_k,
                                        int64_t max_q, int64_t max_k, int64_t rel_extent,
                                        bool causal, int64_t window_left, double softmax_scale,
                                        bool return_lse, int64_t flags) {
+  TORCH_CHECK(k.scalar_type() != at::kFloat8_e4m3fn,
+              "inkling_fa4.fwd: fp8 K/V is supported by decode only");
   ifa4_args a = make_args(q, k, v, rel, cu_q, cu_k, max_q, max_k, rel_extent, causal,
                           window_left, softmax_scale, flags);
   at::Tensor out = at::empty_like(q, q.options().memory_format(at::MemoryFormat::Contiguous));
@@ -130,7 +143,7 @@ std::tuple<at::Tensor, at::Tensor> decode(const at::Tensor& q, const at::Tensor&
                                           int64_t max_q, int64_t max_k, int64_t rel_extent,
                                           bool causal, int64_t window_left,
                                           double softmax_scale, bool return_lse,
-                                          int64_t flags) {
+                                          int64_t flags, double k_scale, double v_scale) {
   ifa4_args a = make_args(q, k, v, rel, cu_q, cu_k, max_q, max_k, rel_extent, causal,
                           window_left, softmax_scale, flags);
   at::Tensor out = at::empty_like(q, q.options().memory_format(at::MemoryFormat::Contiguous));
@@ -143,16 +156,22 @@ std::tuple<at::Tensor, at::Tensor> decode(const at::Tensor& q, const at::Tensor&
     a.lse = lse.data_ptr<float>();
     a.lse_stride_h = lse.stride(0);
   }
-  check_status(ifa4_validate(&a), "decode");
-  const size_t ws_bytes = ifa4_decode_workspace_bytes(&a);
-  TORCH_CHECK(ws_bytes > 0 || a.batch == 0,
-              "inkling_fa4.decode: needs exactly one query token per sequence and "
-              "n_heads / kv_heads <= 16");
+  const bool kv_fp8 = k.scalar_type() == at::kFloat8_e4m3fn;
+  const ifa4_kv_quant qt = kv_quant(k_scale, v_scale);
+  if (!kv_fp8) check_status(ifa4_validate(&a), "decode");
+  const size_t ws_bytes = kv_fp8 ? ifa4_decode_quant_workspace_bytes(&a, nullptr, &qt)
+                                 : ifa4_decode_workspace_bytes(&a);
+  if (ws_bytes == 0 && a.batch > 0)  // invalid arguments: the call reports which status
+    check_status(kv_fp8 ? ifa4_decode_quant_fwd(&a, nullptr, &qt, nullptr, 0, nullptr)
+                        : ifa4_decode_fwd(&a, nullptr, 0, nullptr),
+                 "decode");
   at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes) + 256}, q.options().dtype(at::kByte));
   const uintptr_t base = reinterpret_cast<uintptr_t>(ws.data_ptr());
   void* aligned_ws = reinterpret_cast<void*>((base + 255) / 256 * 256);
   const hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
-  check_status(ifa4_decode_fwd(&a, aligned_ws, ws_bytes, stream), "decode");
+  check_status(kv_fp8 ? ifa4_decode_quant_fwd(&a, nullptr, &qt, aligned_ws, ws_bytes, stream)
+                      : ifa4_decode_fwd(&a, aligned_ws, ws_bytes, stream),
+               "decode");
   return {out, lse};
 }
 
@@ -163,7 +182,8 @@ std::tuple<at::Tensor, at::Tensor> decode_paged(
     const at::Tensor& q, const at::Tensor& k_cache, const at::Tensor& v_cache,
     const at::Tensor& rel, const at::Tensor& cu_q, const at::Tensor& seqused_k,
     const at::Tensor& block_table, int64_t max_q, int64_t max_k, int64_t rel_extent, bool causal,
-    int64_t window_left, double softmax_scale, bool return_lse, int64_t flags) {
+    int64_t window_left, double softmax_scale, bool return_lse, int64_t flags, double k_scale,
+    double v_scale) {
   TORCH_CHECK(k_cache.dim() == 4 && v_cache.dim() == 4,
               "inkling_fa4.decode_paged: k_cache / v_cache must be "
               "[num_blocks, block_size, kv_heads, head_dim]");
@@ -211,14 +231,21 @@ std::tuple<at::Tensor, at::Tensor> decode_paged(
     a.lse = lse.data_ptr<float>();
     a.lse_stride_h = lse.stride(0);
   }
-  const size_t ws_bytes = ifa4_decode_paged_workspace_bytes(&a, &kv);
+  const bool kv_fp8 = k_cache.scalar_type() == at::kFloat8_e4m3fn;
+  const ifa4_kv_quant qt = kv_quant(k_scale, v_scale);
+  const size_t ws_bytes = kv_fp8 ? ifa4_decode_quant_workspace_bytes(&a, &kv, &qt)
+                                 : ifa4_decode_paged_workspace_bytes(&a, &kv);
   if (ws_bytes == 0 && a.batch > 0)  // invalid arguments: the call reports which status
-    check_status(ifa4_decode_paged_fwd(&a, &kv, nullptr, 0, nullptr), "decode_paged");
+    check_status(kv_fp8 ? ifa4_decode_quant_fwd(&a, &kv, &qt, nullptr, 0, nullptr)
+                        : ifa4_decode_paged_fwd(&a, &kv, nullptr, 0, nullptr),
+                 "decode_paged");
   at::Tensor ws = at::empty({static_cast<int64_t>(ws_bytes) + 256}, q.options().dtype(at::kByte));
   const uintptr_t base = reinterpret_cast<uintptr_t>(ws.data_ptr());
   void* aligned_ws = reinterpret_cast<void*>((base + 255) / 256 * 256);
   const hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
-  check_status(ifa4_decode_paged_fwd(&a, &kv, aligned_ws, ws_bytes, stream), "decode_paged");
+  check_status(kv_fp8 ? ifa4_decode_quant_fwd(&a, &kv, &qt, aligned_ws, ws_bytes, stream)
+                      : ifa4_decode_paged_fwd(&a, &kv, aligned_ws, ws_bytes, stream),
+               "decode_paged");
   return {out, lse};
 }
 
@@ -232,12 +259,13 @@ TORCH_LIBRARY(inkling_fa4, m) {
   m.def(
       "decode(Tensor q, Tensor k, Tensor v, Tensor rel_logits, Tensor cu_seqlens_q, "
       "Tensor cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, int rel_extent, bool causal, "
-      "int window_left, float softmax_scale, bool return_lse, int flags) -> (Tensor, Tensor)");
+      "int window_left, float softmax_scale, bool return_lse, int flags, float k_scale, "
+      "float v_scale) -> (Tensor, Tensor)");
   m.def(
       "decode_paged(Tensor q, Tensor k_cache, Tensor v_cache, Tensor rel_logits, "
       "Tensor cu_seqlens_q, Tensor seqused_k, Tensor block_table, int max_seqlen_q, "
       "int max_seqlen_k, int rel_extent, bool causal, int window_left, float softmax_scale, "
-      "bool return_lse, int flags) -> (Tensor, Tensor)");
+      "bool return_lse, int flags, float k_scale, float v_scale) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(inkling_fa4, CUDA, m) {

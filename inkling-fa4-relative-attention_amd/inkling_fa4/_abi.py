@@ -20,6 +20,7 @@ IFA4_ELAUNCH = 4
 IFA4_BF16 = 0
 IFA4_FP16 = 1
 IFA4_FP32 = 2
+IFA4_FP8_E4M3 = 3
 
 IFA4_FLAG_NO_PRUNE = 0x1
 IFA4_FLAG_BOTTOM_RIGHT = 0x2
@@ -68,8 +69,14 @@ class Ifa4PagedKV(ctypes.Structure):
     ]
 
 
+class Ifa4KvQuant(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("kv_dtype", _c_int32),
+                ("k_scale", ctypes.c_float), ("v_scale", ctypes.c_float)]
+
+
 _P_ARGS = ctypes.POINTER(Ifa4Args)
 _P_PAGED = ctypes.POINTER(Ifa4PagedKV)
+_P_QUANT = ctypes.POINTER(Ifa4KvQuant)
 _P_TILE = ctypes.POINTER(Ifa4Tile)
 _P_I32 = ctypes.POINTER(ctypes.c_int32)
 _P_I64 = ctypes.POINTER(ctypes.c_int64)
@@ -86,6 +93,9 @@ SIGNATURES = {
     "ifa4_decode_fwd": (_c_int32, [_P_ARGS, _vp, ctypes.c_size_t, _vp]),
     "ifa4_decode_paged_workspace_bytes": (ctypes.c_size_t, [_P_ARGS, _P_PAGED]),
     "ifa4_decode_paged_fwd": (_c_int32, [_P_ARGS, _P_PAGED, _vp, ctypes.c_size_t, _vp]),
+    "ifa4_decode_quant_workspace_bytes": (ctypes.c_size_t, [_P_ARGS, _P_PAGED, _P_QUANT]),
+    "ifa4_decode_quant_fwd": (_c_int32, [_P_ARGS, _P_PAGED, _P_QUANT, _vp, ctypes.c_size_t,
+                                         _vp]),
 }
 
 _lib = None
@@ -131,6 +141,17 @@ def make_paged(**kw):
     for k, v in kw.items():
         setattr(kv, k, v)
     return kv
+
+
+def make_quant(**kw):
+    """Ifa4KvQuant with struct_size filled (fp8 e4m3, scales 1), fields from kw."""
+    qt = Ifa4KvQuant()
+    qt.struct_size = ctypes.sizeof(Ifa4KvQuant)
+    qt.kv_dtype = IFA4_FP8_E4M3
+    qt.k_scale = qt.v_scale = 1.0
+    for k, v in kw.items():
+        setattr(qt, k, v)
+    return qt
 
 
 def prefill_tile(head_dim):

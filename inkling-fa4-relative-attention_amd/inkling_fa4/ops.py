@@ -98,15 +98,22 @@ def inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqle
                                      max_seqlen_q, max_seqlen_k, rel_extent, causal=True,
                                      window_size=(-1, -1), n_heads=None, kv_heads=None,
                                      head_dim=None, arch=None, *, softmax_scale=None,
-                                     return_lse=False, bottom_right=False):
+                                     return_lse=False, bottom_right=False, k_scale=1.0,
+                                     v_scale=1.0):
     """Decode forward: exactly one query token per sequence
     (cu_seqlens_q == arange(batch + 1)), KV split across workgroups and merged
     by log-sum-exp.  Falls through to the prefill kernel when q holds more
-    tokens than there are sequences, or for GQA groups above 16."""
+    tokens than there are sequences, or for GQA groups above 16.
+
+    k / v may be torch.float8_e4m3fn (an FP8 KV cache, GQA groups up to 8):
+    the keys and values are k * k_scale and v * v_scale.
+    """
     scale = _resolve(q, k, n_heads, kv_heads, head_dim, softmax_scale)
     batch = cu_seqlens_q.shape[0] - 1
     group = q.shape[1] // k.shape[1]
     if q.shape[0] != batch or group > 16:
+        if k.dtype == torch.float8_e4m3fn:
+            raise ValueError("fp8 K/V needs one query per sequence and GQA groups up to 8")
         return inkling_fa4_rel_attention(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
                                          max_seqlen_q, max_seqlen_k, rel_extent, causal,
                                          window_size, softmax_scale=scale,
@@ -114,7 +121,7 @@ def inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqle
     out, lse = _ops().decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
                              int(max_seqlen_q), int(max_seqlen_k), int(rel_extent), bool(causal),
                              _window_left(window_size), scale, bool(return_lse),
-                             _flag_bits(bottom_right))
+                             _flag_bits(bottom_right), float(k_scale), float(v_scale))
     return (out, lse) if return_lse else out
 
 
@@ -123,7 +130,7 @@ def inkling_fa4_rel_attention_decode_paged(q, k_cache, v_cache, rel_logits, cu_s
                                            seqused_k, block_table, max_seqlen_q, max_seqlen_k,
                                            rel_extent, causal=True, window_size=(-1, -1), *,
                                            softmax_scale=None, return_lse=False,
-                                           bottom_right=False):
+                                           bottom_right=False, k_scale=1.0, v_scale=1.0):
     """Decode over a paged KV cache (the serving backend's format,
     outputs/architecture.md:117-120: blocks of 16 tokens).
 
@@ -133,7 +140,9 @@ def inkling_fa4_rel_attention_decode_paged(q, k_cache, v_cache, rel_logits, cu_s
     j % block_size), seqused_k int32 [batch] keys per sequence; one query per
     sequence (cu_seqlens_q == arange(batch + 1)), GQA groups up to 16.
     Results equal inkling_fa4_rel_attention_decode on the same keys stored
-    contiguously (bit for bit).  max_seqlen_k must bound seqused_k.
+    contiguously (bit for bit).  max_seqlen_k must bound seqused_k.  An fp8
+    cache (torch.float8_e4m3fn, with k_scale / v_scale) needs blocks of at
+    least 16 tokens when head_dim is 64.
     """
     if k_cache.dim() != 4:
         raise ValueError("k_cache must be [num_blocks, block_size, kv_heads, head_dim]")
@@ -141,7 +150,8 @@ def inkling_fa4_rel_attention_decode_paged(q, k_cache, v_cache, rel_logits, cu_s
     out, lse = _ops().decode_paged(q, k_cache, v_cache, rel_logits, cu_seqlens_q, seqused_k,
                                    block_table, int(max_seqlen_q), int(max_seqlen_k),
                                    int(rel_extent), bool(causal), _window_left(window_size),
-                                   scale, bool(return_lse), _flag_bits(bottom_right))
+                                   scale, bool(return_lse), _flag_bits(bottom_right),
+                                   float(k_scale), float(v_scale))
     return (out, lse) if return_lse else out
 
 

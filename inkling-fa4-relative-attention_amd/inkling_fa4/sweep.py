@@ -13,7 +13,8 @@ Two steps, so that variants are built where hipcc is and timed where the GPU is:
         [--counters SQ_VALU_MFMA_BUSY_CYCLES,GRBM_GUI_ACTIVE] [--out table.md]
 
 `build` writes one sub-directory per grid point holding libifa4.so, a copy of the
-torch binding (it loads the libifa4.so next to it) and knobs.json.  `run` first
+torch binding (it loads the libifa4.so next to it), knobs.json and the digest of
+the sources (one snapshot per call: edits during the build do not leak in).  `run` first
 runs the in-tree build, then each variant in a child process with IFA4_LIB_DIR
 pointing at its directory; a variant whose output on a small case differs from
 the in-tree build's (atol 2e-2 on out, 1e-3 on lse) is reported and not timed.
@@ -28,6 +29,7 @@ Knobs (macros of the kernel sources):
   tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
 """
 import argparse
+import hashlib
 import itertools
 import json
 import os
@@ -54,6 +56,18 @@ def _grid_points(specs):
     return [dict(zip(names, combo)) for combo in itertools.product(*values)]
 
 
+def _source_digest(csrc, include):
+    h = hashlib.sha256()
+    for d in (csrc, include):
+        for name in sorted(os.listdir(d)):
+            path = os.path.join(d, name)
+            if os.path.isfile(path) and name.endswith((".hip", ".cpp", ".h", ".hpp")):
+                h.update(name.encode())
+                with open(path, "rb") as f:
+                    h.update(f.read())
+    return h.hexdigest()[:12]
+
+
 def cmd_build(args):
     sys.path.insert(0, _PKG_ROOT)
     import build as b  # inkling-fa4-relative-attention_amd/build.py
@@ -62,16 +76,25 @@ def cmd_build(args):
     if not os.path.exists(ext):
         raise SystemExit(f"{ext} is missing: build the package first (build.py)")
     os.makedirs(args.dir, exist_ok=True)
-    for knobs in _grid_points(args.grid):
-        name = "_".join(f"{k.replace('IFA4_', '').lower()}{v}" for k, v in knobs.items())
-        out = os.path.join(args.dir, name)
-        with tempfile.TemporaryDirectory() as tmp:
-            b.build_library(args.jobs, out_dir=out,
-                            defines=[f"{k}={v}" for k, v in knobs.items()], build_dir=tmp)
-        shutil.copy2(ext, os.path.join(out, b.EXT_NAME))
-        with open(os.path.join(out, "knobs.json"), "w") as f:
-            json.dump(knobs, f)
-        print(f"built {out}  {knobs}", flush=True)
+    with tempfile.TemporaryDirectory() as snap:
+        # every variant of this call is built from one copy of the sources, so
+        # an edit while the grid builds cannot mix two versions in one library
+        csrc = shutil.copytree(b.CSRC, os.path.join(snap, "csrc"))
+        include = shutil.copytree(b.INCLUDE, os.path.join(snap, "include"))
+        digest = _source_digest(csrc, include)
+        for knobs in _grid_points(args.grid):
+            name = "_".join(f"{k.replace('IFA4_', '').lower()}{v}" for k, v in knobs.items())
+            out = os.path.join(args.dir, name)
+            with tempfile.TemporaryDirectory() as tmp:
+                b.build_library(args.jobs, out_dir=out,
+                                defines=[f"{k}={v}" for k, v in knobs.items()], build_dir=tmp,
+                                csrc=csrc, include=include)
+            shutil.copy2(ext, os.path.join(out, b.EXT_NAME))
+            with open(os.path.join(out, "knobs.json"), "w") as f:
+                json.dump(knobs, f)
+            with open(os.path.join(out, "source.txt"), "w") as f:
+                f.write(digest + "\n")
+            print(f"built {out}  {knobs}  sources {digest}", flush=True)
     return 0
 
 
@@ -135,11 +158,17 @@ def cmd_run(args):
     import torch
 
     variants = [("in-tree", None, {})]
+    sources = set()
     for name in sorted(os.listdir(args.dir)):
         d = os.path.join(args.dir, name)
         if os.path.exists(os.path.join(d, "knobs.json")):
             with open(os.path.join(d, "knobs.json")) as f:
                 variants.append((name, d, json.load(f)))
+            src = os.path.join(d, "source.txt")
+            sources.add(open(src).read().strip() if os.path.exists(src) else "?")
+    if len(sources) > 1:
+        print(f"warning: variants were built from different sources {sorted(sources)}",
+              file=sys.stderr, flush=True)
     kernel = "prefill_fwd_kernel" if args.workload == "prefill" else "decode_stream_kernel"
     rows, ref = [], None
     with tempfile.TemporaryDirectory() as tmp:

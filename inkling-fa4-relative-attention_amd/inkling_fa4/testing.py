@@ -180,3 +180,19 @@ def paginate(case, block_size=16, seed=0, spare_blocks=5, fill=float("nan"),
             kc[blk, :rows] = case.k[src:src + rows]
             vc[blk, :rows] = case.v[src:src + rows]
     return PagedKV(kc, vc, table, torch.tensor(lens, dtype=torch.int32))
+
+
+def fp8_kv(case, k_scale=None, v_scale=None):
+    """FP8 (OCP e4m3, torch.float8_e4m3fn) copy of a case's K/V with one scale
+    per tensor (default: the tensor's max magnitude maps to 448).  Returns
+    (k8, v8, k_scale, v_scale, dequantised case); the dequantised case holds
+    k8 * k_scale and v8 * v_scale in fp32, the exact values the kernel sees."""
+    def scale_of(t):
+        m = float(t.float().abs().max())
+        return (m / 448.0) if m > 0 else 1.0
+    ks = scale_of(case.k) if k_scale is None else float(k_scale)
+    vs = scale_of(case.v) if v_scale is None else float(v_scale)
+    k8 = (case.k.float() / ks).to(torch.float8_e4m3fn)
+    v8 = (case.v.float() / vs).to(torch.float8_e4m3fn)
+    deq = replace(case, k=k8.float() * ks, v=v8.float() * vs)
+    return k8, v8, ks, vs, deq

@@ -274,3 +274,35 @@ def test_pruning_bottom_right_visits_exactly_the_tiles_with_visible_pairs(seed):
     need = _needed_tiles(lens_q, lens_k, causal, window, t.block_q, t.block_k,
                          bottom_right=True)
     assert visited == need
+
+
+@pytest.mark.parametrize("kw,qkw,paged,expect", [
+    ({}, {}, False, _abi.IFA4_OK),
+    ({}, {}, True, _abi.IFA4_OK),
+    ({}, {"kv_dtype": _abi.IFA4_BF16}, False, _abi.IFA4_EUNSUPPORTED),
+    ({}, {"k_scale": 0.0}, False, _abi.IFA4_EINVAL),
+    ({}, {"v_scale": float("nan")}, False, _abi.IFA4_EINVAL),
+    ({}, {"struct_size": 4}, False, _abi.IFA4_EINVAL),
+    ({"n_heads": 16, "kv_heads": 1}, {}, False, _abi.IFA4_EUNSUPPORTED),  # fp8: groups <= 8
+    ({"k_stride_t": 2 * 128 + 8}, {}, False, _abi.IFA4_EUNSUPPORTED),      # 16-byte fp8 rows
+    ({"k_stride_t": 2 * 128 + 16}, {}, False, _abi.IFA4_OK),
+    ({"head_dim": 64, "q_stride_h": 64, "k_stride_h": 64, "v_stride_h": 64,
+      "out_stride_h": 64, "k_stride_t": 128, "v_stride_t": 128}, {}, True,
+     _abi.IFA4_EUNSUPPORTED),                                               # D 64 fp8: blocks >= 16
+])
+def test_quant_validation(kw, qkw, paged, expect):
+    lib = _abi.lib()
+    a = _decode_args(cu_seqlens_k=7 * _P, total_k=600000, **kw)
+    kv = _paged_ok(block_size=8, max_blocks_per_seq=2048) if paged else None
+    qt = _abi.make_quant(k_scale=0.01, v_scale=0.02)
+    for k, v in qkw.items():
+        setattr(qt, k, v)
+    kv_ref = ctypes.byref(kv) if kv is not None else None
+    ws = lib.ifa4_decode_quant_workspace_bytes(ctypes.byref(a), kv_ref, ctypes.byref(qt))
+    assert (ws > 0) == (expect == _abi.IFA4_OK)
+    st = lib.ifa4_decode_quant_fwd(ctypes.byref(a), kv_ref, ctypes.byref(qt), None, 0, None)
+    assert st == (_abi.IFA4_EWORKSPACE if expect == _abi.IFA4_OK else expect)
+    if expect == _abi.IFA4_OK and not paged:
+        assert ws == lib.ifa4_decode_workspace_bytes(ctypes.byref(a))
+    assert lib.ifa4_decode_quant_fwd(ctypes.byref(a), kv_ref, None, 256, 1 << 30, None) == \
+        _abi.IFA4_EINVAL

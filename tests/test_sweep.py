@@ -56,7 +56,9 @@ def test_variant_build_carries_its_knob(tmp_path):
     sweep.main(["build", "--dir", str(tmp_path), "--grid", "IFA4_DECODE_WAVES=512",
                 "--jobs", "3"])
     vdir = tmp_path / "decode_waves512"
-    assert sorted(os.listdir(vdir)) == ["_ifa4_torch.so", "knobs.json", "libifa4.so"]
+    assert sorted(os.listdir(vdir)) == ["_ifa4_torch.so", "knobs.json", "libifa4.so",
+                                        "source.txt"]
+    assert len((vdir / "source.txt").read_text().strip()) == 12
     assert json.loads((vdir / "knobs.json").read_text()) == {"IFA4_DECODE_WAVES": "512"}
     steps = 64 * 2 * (16384 // 32)
     default, variant = _tile(), _tile(str(vdir))
