@@ -149,7 +149,8 @@ int32_t ifa4_prefill_count_tiles(const ifa4_args* args, const int32_t* host_cu_s
 
 /*
  * Decode: exactly one query token per sequence (total_q == batch).  Split-KV,
- * stream-K: pass 1 runs min(2048, steps) persistent waves over all
+ * stream-K: pass 1 runs min(W, steps) persistent waves (W from the tile table:
+ * 896 for 16-bit K/V, 2048 for fp8; ifa4_decode_tile reports it) over all
  * (sequence, kv head) caches laid end to end in 32-key steps, each wave an
  * equal range; it writes one (o, lse) partial per (cache, wave) it touches
  * into the workspace.  Pass 2 merges each cache's partials by log-sum-exp and

@@ -152,8 +152,8 @@ bool key0_only(const ifa4_args* a) {
   return a->causal != 0 && (a->flags & IFA4_FLAG_BOTTOM_RIGHT) == 0;
 }
 
-int32_t decode_waves(const ifa4_args* a) {
-  return ifa4::decode_waves_for(a->batch, a->kv_heads, a->max_seqlen_k, key0_only(a));
+int32_t decode_waves(const ifa4_args* a, bool fp8 = false) {
+  return ifa4::decode_waves_for(a->batch, a->kv_heads, a->max_seqlen_k, key0_only(a), fp8);
 }
 
 // Decode workspace: partial (o, lse) slots, one per (segment, wave) pair that
@@ -162,11 +162,11 @@ struct DecodeLayout {
   int64_t slots, o_bytes, lse_bytes, meta_bytes;
   int64_t total() const { return o_bytes + lse_bytes + meta_bytes; }
 };
-DecodeLayout decode_layout(const ifa4_args* a) {
+DecodeLayout decode_layout(const ifa4_args* a, bool fp8 = false) {
   DecodeLayout l;
   const int64_t segs = (int64_t)a->batch * a->kv_heads;
   const int64_t group = a->n_heads / a->kv_heads;
-  l.slots = segs + decode_waves(a);
+  l.slots = segs + decode_waves(a, fp8);
   l.o_bytes = (l.slots * group * a->head_dim * 4 + 255) / 256 * 256;
   l.lse_bytes = (l.slots * group * 4 + 255) / 256 * 256;
   l.meta_bytes = segs * 2 * 4;
@@ -202,7 +202,7 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
   const int32_t st = check_decode(args, kv, qt);
   if (st != IFA4_OK) return st;
   if (args->batch == 0) return IFA4_OK;
-  const DecodeLayout lay = decode_layout(args);
+  const DecodeLayout lay = decode_layout(args, qt != nullptr);
   if (workspace == nullptr || workspace_bytes < (size_t)lay.total() || !aligned(workspace, 256))
     return IFA4_EWORKSPACE;
 
@@ -239,7 +239,7 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
   p.bottom_right = (args->flags & IFA4_FLAG_BOTTOM_RIGHT) ? 1 : 0;
   p.window_left = args->window_left;
   p.rel_dtype = args->rel_dtype;
-  p.n_waves = decode_waves(args);
+  p.n_waves = decode_waves(args, qt != nullptr);
   p.kv_fp8 = qt != nullptr ? 1 : 0;
   p.scale_log2 = args->softmax_scale * (qt != nullptr ? qt->k_scale : 1.f) * kLog2eHost;
   p.v_scale = qt != nullptr ? qt->v_scale : 1.f;
@@ -380,7 +380,7 @@ int32_t ifa4_decode_paged_fwd(const ifa4_args* args, const ifa4_paged_kv* kv, vo
 size_t ifa4_decode_quant_workspace_bytes(const ifa4_args* args, const ifa4_paged_kv* kv,
                                          const ifa4_kv_quant* quant) {
   if (quant == nullptr || check_decode(args, kv, quant) != IFA4_OK) return 0;
-  return (size_t)decode_layout(args).total();
+  return (size_t)decode_layout(args, true).total();
 }
 
 int32_t ifa4_decode_quant_fwd(const ifa4_args* args, const ifa4_paged_kv* kv,

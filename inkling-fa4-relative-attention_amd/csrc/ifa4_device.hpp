@@ -197,6 +197,25 @@ __device__ __forceinline__ void dma_16(rsrc_t r, uint32_t byte_off, const void* 
                : "memory");
 }
 
+// Same DMA with the wave-uniform part of the offset in the instruction's scalar
+// offset (soffset) and the LDS byte address already in an SGPR value: the
+// caller keeps the per-lane offset in a register across tiles and does the
+// per-tile arithmetic on the scalar unit.  The caller issues s_nop 4 once before
+// a batch (VALU-written SGPR -> VMEM hazard, as for dma_16); the s_nop 0 here
+// covers the SALU write of M0.
+__device__ __forceinline__ void dma_16_so(rsrc_t r, uint32_t lane_off, uint32_t soffset,
+                                          uint32_t lds_addr) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(lane_off), "s"(r),
+               "s"(soffset), "{m0}"(lds_addr)
+               : "memory");
+}
+__device__ __forceinline__ void hazard_nop5() { asm volatile("s_nop 4" ::: "memory"); }
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // Bias element types: storage size and conversion of the loaded bits to fp32.
 struct RelF32 {
   static constexpr int kBytes = 4;

@@ -75,6 +75,9 @@
 #ifndef IFA4_PVALU
 #define IFA4_PVALU 7
 #endif
+#ifndef IFA4_DMA2
+#define IFA4_DMA2 1
+#endif
 
 namespace ifa4 {
 namespace {
@@ -257,6 +260,38 @@ void prefill_fwd_kernel(PrefillParams p) {
   // slot L % kChunks of row L / kChunks with the chunk that swizzles to it.
   const int dma_row = lane / St::kChunks;
   const int dma_slot = lane % St::kChunks;
+#if IFA4_DMA2
+  // Each wave DMAs rows of one tensor (K for the first half of the waves, V for
+  // the second).  A lane's offset within a DMA depends on the tile only through
+  // kb (added as the scalar offset) and on the block only through the swizzle
+  // phase (blk % kPhases) and a row shift (also scalar): kPhases registers, set once.
+  constexpr int kPhases = 16 / St::kRowsPerDma;
+  static_assert(St::kDmaPerWave <= St::kDmaPerTensor && St::kDmaPerTensor % St::kDmaPerWave == 0,
+                "a wave's DMAs stay within one tensor");
+  const bool dma_v = wave * St::kDmaPerWave >= St::kDmaPerTensor;
+  const uint32_t dma_rowb = dma_v ? v_row : k_row;
+  const rsrc_t dma_r = dma_v ? rv : rk;
+  uint32_t dma_voff[kPhases];
+#pragma unroll
+  for (int ph = 0; ph < kPhases; ++ph) {
+    const int row = ph * St::kRowsPerDma + dma_row;
+    dma_voff[ph] = (uint32_t)dma_row * dma_rowb + 16u * (uint32_t)(dma_slot ^ swz<St::kChunks>(row));
+  }
+  const uint32_t lds_stages = lds_addr(stages);
+  auto dma_tile = [&](int kt, uint16_t* stage) {
+    const int kb = kt * kBlockK;
+    const uint32_t stage_lds = lds_stages + (uint32_t)((stage - stages) * 2);
+    hazard_nop5();
+#pragma unroll
+    for (int u = 0; u < St::kDmaPerWave; ++u) {
+      const int id = wave * St::kDmaPerWave + u;
+      const int blk = dma_v ? id - St::kDmaPerTensor : id;
+      const uint32_t soff = (uint32_t)(kb + blk * St::kRowsPerDma) * dma_rowb;
+      const uint32_t dst = stage_lds + (uint32_t)(((dma_v ? St::kTile : 0) + blk * 512) * 2);
+      dma_16_so(dma_r, dma_voff[u % kPhases], soff, dst);
+    }
+  };
+#else
   auto dma_tile = [&](int kt, uint16_t* stage) {
     const int kb = kt * kBlockK;
 #pragma unroll
@@ -271,6 +306,7 @@ void prefill_fwd_kernel(PrefillParams p) {
       dma_16(is_v ? rv : rk, off, dst);
     }
   };
+#endif
 
   // Bias resource: the (sequence, head) rows of the bias; each lane reads its rows.
   const rsrc_t rrel = make_rsrc(

@@ -30,10 +30,18 @@ constexpr PrefillTileEntry kPrefillTiles[] = {
     {128, 128, 64, 4, 2},
 };
 
+// Persistent waves of the decode stream pass (at most; never more than the
+// steps).  Measured on the 64-sequence batch (KV 1K-16K, bf16, non-causal):
+// 768-896 waves 0.112 ms, 1024 0.113, 2048 0.117, 512 0.148 (too few bytes in
+// flight).  inkling_fa4.sweep with IFA4_DECODE_WAVES / IFA4_DECODE_WAVES_FP8.
 #ifndef IFA4_DECODE_WAVES
-#define IFA4_DECODE_WAVES 2048
+#define IFA4_DECODE_WAVES 896
+#endif
+#ifndef IFA4_DECODE_WAVES_FP8
+#define IFA4_DECODE_WAVES_FP8 2048
 #endif
 constexpr int64_t kDecodeWaves = IFA4_DECODE_WAVES;
+constexpr int64_t kDecodeWavesFp8 = IFA4_DECODE_WAVES_FP8;
 constexpr int32_t kDecodeStep = 32;  // keys per step of a decode wave
 
 // Upper bound of the 32-key steps of a decode call: every (sequence, kv head)
@@ -46,9 +54,10 @@ inline int64_t decode_max_steps(int64_t batch, int64_t kv_heads, int64_t max_seq
 }
 
 inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seqlen_k,
-                                bool key0_only) {
+                                bool key0_only, bool fp8) {
   const int64_t t = decode_max_steps(batch, kv_heads, max_seqlen_k, key0_only);
-  return (int32_t)(t < kDecodeWaves ? t : kDecodeWaves);
+  const int64_t w = fp8 ? kDecodeWavesFp8 : kDecodeWaves;
+  return (int32_t)(t < w ? t : w);
 }
 
 }  // namespace ifa4

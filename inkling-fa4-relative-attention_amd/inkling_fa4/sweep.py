@@ -27,6 +27,7 @@ Knobs (macros of the kernel sources):
                    IFA4_BIAS_LDS              shared bias table in LDS (0/1)
                    IFA4_PREFILL_NQB           32-row blocks per wave (1/2)
   tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
+                   IFA4_DECODE_WAVES_FP8      the same for an fp8 KV cache (workload decode_fp8)
 """
 import argparse
 import hashlib
@@ -112,12 +113,17 @@ def _case(workload, seq):
 
 
 def _call(workload, case, return_lse):
-    from inkling_fa4 import inkling_fa4_rel_attention, inkling_fa4_rel_attention_decode
+    from inkling_fa4 import inkling_fa4_rel_attention, inkling_fa4_rel_attention_decode, testing
 
     fn = inkling_fa4_rel_attention if workload == "prefill" else inkling_fa4_rel_attention_decode
     args = case.args()
+    kw = {}
+    if workload == "decode_fp8":  # the same keys as an fp8 cache, per-tensor scales
+        k8, v8, ks, vs, _ = testing.fp8_kv(case)
+        args = (args[0], k8, v8) + args[3:]
+        kw = {"k_scale": ks, "v_scale": vs}
     return lambda: fn(*args, causal=case.causal, window_size=case.window_size,
-                      softmax_scale=case.scale, return_lse=return_lse)
+                      softmax_scale=case.scale, return_lse=return_lse, **kw)
 
 
 def cmd_measure(args):
@@ -239,7 +245,8 @@ def main(argv=None):
     b.add_argument("--jobs", type=int, default=4)
     for name in ("run", "measure"):
         r = sub.add_parser(name)
-        r.add_argument("--workload", choices=["prefill", "decode"], default="prefill")
+        r.add_argument("--workload", choices=["prefill", "decode", "decode_fp8"],
+                       default="prefill")
         r.add_argument("--seq", type=int, default=4096)
         r.add_argument("--steps", type=int, default=30)
         r.add_argument("--warmup", type=int, default=5)

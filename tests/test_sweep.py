@@ -63,5 +63,5 @@ def test_variant_build_carries_its_knob(tmp_path):
     steps = 64 * 2 * (16384 // 32)
     default, variant = _tile(), _tile(str(vdir))
     assert variant["lib"] == str(vdir / "libifa4.so")
-    assert default["kv_chunk"] == 32 * -(-steps // 2048)
+    assert default["kv_chunk"] == 32 * -(-steps // 896)
     assert variant["kv_chunk"] == 32 * -(-steps // 512)
