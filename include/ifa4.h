@@ -195,8 +195,9 @@ typedef struct ifa4_paged_kv {
 
 /*
  * Decode over a paged KV cache: the same two passes as ifa4_decode_fwd with
- * the same workspace layout, results bit-identical to ifa4_decode_fwd on the
- * same keys stored contiguously.  Replaces the KV-cache read of the serving
+ * the same workspace layout (more partial slots: a paged cache streams with up
+ * to 2048 waves), results equal to ifa4_decode_fwd on the same keys stored
+ * contiguously up to the order of the split merge.  Replaces the KV-cache read of the serving
  * backend's flash_attn_varlen_func call (block_table / seqused_k arguments),
  * outputs/architecture.md:117-120.
  */

@@ -152,8 +152,9 @@ bool key0_only(const ifa4_args* a) {
   return a->causal != 0 && (a->flags & IFA4_FLAG_BOTTOM_RIGHT) == 0;
 }
 
-int32_t decode_waves(const ifa4_args* a, bool fp8 = false) {
-  return ifa4::decode_waves_for(a->batch, a->kv_heads, a->max_seqlen_k, key0_only(a), fp8);
+int32_t decode_waves(const ifa4_args* a, bool fp8 = false, bool paged = false) {
+  return ifa4::decode_waves_for(a->batch, a->kv_heads, a->max_seqlen_k, key0_only(a), fp8,
+                                paged);
 }
 
 // Decode workspace: partial (o, lse) slots, one per (segment, wave) pair that
@@ -162,11 +163,11 @@ struct DecodeLayout {
   int64_t slots, o_bytes, lse_bytes, meta_bytes;
   int64_t total() const { return o_bytes + lse_bytes + meta_bytes; }
 };
-DecodeLayout decode_layout(const ifa4_args* a, bool fp8 = false) {
+DecodeLayout decode_layout(const ifa4_args* a, bool fp8 = false, bool paged = false) {
   DecodeLayout l;
   const int64_t segs = (int64_t)a->batch * a->kv_heads;
   const int64_t group = a->n_heads / a->kv_heads;
-  l.slots = segs + decode_waves(a, fp8);
+  l.slots = segs + decode_waves(a, fp8, paged);
   l.o_bytes = (l.slots * group * a->head_dim * 4 + 255) / 256 * 256;
   l.lse_bytes = (l.slots * group * 4 + 255) / 256 * 256;
   l.meta_bytes = segs * 2 * 4;
@@ -202,7 +203,7 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
   const int32_t st = check_decode(args, kv, qt);
   if (st != IFA4_OK) return st;
   if (args->batch == 0) return IFA4_OK;
-  const DecodeLayout lay = decode_layout(args, qt != nullptr);
+  const DecodeLayout lay = decode_layout(args, qt != nullptr, kv != nullptr);
   if (workspace == nullptr || workspace_bytes < (size_t)lay.total() || !aligned(workspace, 256))
     return IFA4_EWORKSPACE;
 
@@ -239,7 +240,7 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
   p.bottom_right = (args->flags & IFA4_FLAG_BOTTOM_RIGHT) ? 1 : 0;
   p.window_left = args->window_left;
   p.rel_dtype = args->rel_dtype;
-  p.n_waves = decode_waves(args, qt != nullptr);
+  p.n_waves = decode_waves(args, qt != nullptr, kv != nullptr);
   p.kv_fp8 = qt != nullptr ? 1 : 0;
   p.scale_log2 = args->softmax_scale * (qt != nullptr ? qt->k_scale : 1.f) * kLog2eHost;
   p.v_scale = qt != nullptr ? qt->v_scale : 1.f;
@@ -368,7 +369,7 @@ int32_t ifa4_decode_fwd(const ifa4_args* args, void* workspace, size_t workspace
 
 size_t ifa4_decode_paged_workspace_bytes(const ifa4_args* args, const ifa4_paged_kv* kv) {
   if (check_decode(args, kv) != IFA4_OK) return 0;
-  return (size_t)decode_layout(args).total();
+  return (size_t)decode_layout(args, false, true).total();
 }
 
 int32_t ifa4_decode_paged_fwd(const ifa4_args* args, const ifa4_paged_kv* kv, void* workspace,
@@ -380,7 +381,7 @@ int32_t ifa4_decode_paged_fwd(const ifa4_args* args, const ifa4_paged_kv* kv, vo
 size_t ifa4_decode_quant_workspace_bytes(const ifa4_args* args, const ifa4_paged_kv* kv,
                                          const ifa4_kv_quant* quant) {
   if (quant == nullptr || check_decode(args, kv, quant) != IFA4_OK) return 0;
-  return (size_t)decode_layout(args, true).total();
+  return (size_t)decode_layout(args, true, kv != nullptr).total();
 }
 
 int32_t ifa4_decode_quant_fwd(const ifa4_args* args, const ifa4_paged_kv* kv,

@@ -31,16 +31,25 @@ constexpr PrefillTileEntry kPrefillTiles[] = {
 };
 
 // Persistent waves of the decode stream pass (at most; never more than the
-// steps).  Measured on the 64-sequence batch (KV 1K-16K, bf16, non-causal):
-// 768-896 waves 0.112 ms, 1024 0.113, 2048 0.117, 512 0.148 (too few bytes in
-// flight).  inkling_fa4.sweep with IFA4_DECODE_WAVES / IFA4_DECODE_WAVES_FP8.
+// steps), from the sweep on the 64-sequence batch (KV 1K-16K, non-causal;
+// profiles/sweep_decode_waves_b64.md):
+//   contiguous bf16: 896 waves 0.112 ms, 1024 0.112, 768 0.113, 2048 0.116,
+//                    512 0.151 (too few bytes in flight);
+//   paged (blocks of 16): 2048 0.120, 1024 0.121, 896 0.133, 768 0.149 -- a
+//                    table-window refill stalls the wave, more waves hide it;
+//   fp8 K/V: 2048 0.065, 3072 0.074, 1536 0.078, 1024 0.084 (half the bytes
+//                    per step: more waves for the same bytes in flight).
 #ifndef IFA4_DECODE_WAVES
 #define IFA4_DECODE_WAVES 896
+#endif
+#ifndef IFA4_DECODE_WAVES_PAGED
+#define IFA4_DECODE_WAVES_PAGED 2048
 #endif
 #ifndef IFA4_DECODE_WAVES_FP8
 #define IFA4_DECODE_WAVES_FP8 2048
 #endif
 constexpr int64_t kDecodeWaves = IFA4_DECODE_WAVES;
+constexpr int64_t kDecodeWavesPaged = IFA4_DECODE_WAVES_PAGED;
 constexpr int64_t kDecodeWavesFp8 = IFA4_DECODE_WAVES_FP8;
 constexpr int32_t kDecodeStep = 32;  // keys per step of a decode wave
 
@@ -54,9 +63,11 @@ inline int64_t decode_max_steps(int64_t batch, int64_t kv_heads, int64_t max_seq
 }
 
 inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seqlen_k,
-                                bool key0_only, bool fp8) {
+                                bool key0_only, bool fp8, bool paged) {
   const int64_t t = decode_max_steps(batch, kv_heads, max_seqlen_k, key0_only);
-  const int64_t w = fp8 ? kDecodeWavesFp8 : kDecodeWaves;
+  int64_t w = kDecodeWaves;
+  if (paged && kDecodeWavesPaged > w) w = kDecodeWavesPaged;
+  if (fp8 && kDecodeWavesFp8 > w) w = kDecodeWavesFp8;
   return (int32_t)(t < w ? t : w);
 }
 

@@ -140,7 +140,7 @@ def inkling_fa4_rel_attention_decode_paged(q, k_cache, v_cache, rel_logits, cu_s
     j % block_size), seqused_k int32 [batch] keys per sequence; one query per
     sequence (cu_seqlens_q == arange(batch + 1)), GQA groups up to 16.
     Results equal inkling_fa4_rel_attention_decode on the same keys stored
-    contiguously (bit for bit).  max_seqlen_k must bound seqused_k.  An fp8
+    contiguously, up to the order in which the KV splits are merged.  max_seqlen_k must bound seqused_k.  An fp8
     cache (torch.float8_e4m3fn, with k_scale / v_scale) needs blocks of at
     least 16 tokens when head_dim is 64.
     """

@@ -113,11 +113,19 @@ def _case(workload, seq):
 
 
 def _call(workload, case, return_lse):
-    from inkling_fa4 import inkling_fa4_rel_attention, inkling_fa4_rel_attention_decode, testing
+    from inkling_fa4 import (inkling_fa4_rel_attention, inkling_fa4_rel_attention_decode,
+                             inkling_fa4_rel_attention_decode_paged, testing)
 
     fn = inkling_fa4_rel_attention if workload == "prefill" else inkling_fa4_rel_attention_decode
     args = case.args()
     kw = {}
+    if workload == "decode_paged":  # the same keys in blocks of 16, shuffled
+        pk = testing.paginate(case.to("cpu"), block_size=16, seed=0, spare_blocks=0,
+                              fill=0.0).to(case.q.device)
+        return lambda: inkling_fa4_rel_attention_decode_paged(
+            case.q, pk.k_cache, pk.v_cache, case.rel, case.cu_q, pk.seqused_k, pk.block_table,
+            case.max_q, case.max_k, case.rel_extent, causal=case.causal,
+            window_size=case.window_size, softmax_scale=case.scale, return_lse=return_lse)
     if workload == "decode_fp8":  # the same keys as an fp8 cache, per-tensor scales
         k8, v8, ks, vs, _ = testing.fp8_kv(case)
         args = (args[0], k8, v8) + args[3:]
@@ -245,7 +253,7 @@ def main(argv=None):
     b.add_argument("--jobs", type=int, default=4)
     for name in ("run", "measure"):
         r = sub.add_parser(name)
-        r.add_argument("--workload", choices=["prefill", "decode", "decode_fp8"],
+        r.add_argument("--workload", choices=["prefill", "decode", "decode_fp8", "decode_paged"],
                        default="prefill")
         r.add_argument("--seq", type=int, default=4096)
         r.add_argument("--steps", type=int, default=30)

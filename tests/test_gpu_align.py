@@ -133,5 +133,6 @@ def test_paged_decode_bottom_right(cuda, window):
                                        causal=True, window_left=case.window_or_none,
                                        bottom_right=True)
     _check((out.cpu(), lse.cpu()), want)
-    contiguous = _decode(case, cuda)
-    assert torch.equal(out.cpu(), contiguous[0]) and torch.equal(lse.cpu(), contiguous[1])
+    contiguous = _decode(case, cuda)  # same keys; the split merge may differ in order
+    torch.testing.assert_close(out.cpu().float(), contiguous[0].float(), atol=1e-3, rtol=1e-2)
+    torch.testing.assert_close(lse.cpu(), contiguous[1], atol=1e-5, rtol=0)
