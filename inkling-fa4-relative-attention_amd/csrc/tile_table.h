@@ -5,12 +5,16 @@
 // Prefill: one shape for every sequence length.  The kernel is written for
 // 4 waves x 32 query rows (BLOCK_Q 128) and 64-key KV tiles in two LDS stages
 // (64 KiB of LDS at head_dim 128, so two workgroups fit in the 160 KiB of a
-// CU); the shape is a compile-time property of the kernel, listed here so the
-// host reports what runs.
+// CU; 232 VGPRs, two waves per SIMD); the shape is a compile-time property of
+// the kernel, listed here so the host reports what runs.  Measured on the
+// causal 8 x 4096 workload (profiles/sweep_prefill_knobs_b8_s4096.md): 0.262 ms
+// as listed; 64 rows per wave at one wave per SIMD (PREFILL_NQB 2) 0.469 ms;
+// BLOCK_K 32 and 1-wave-per-SIMD shapes were slower in earlier builds.  The
+// counters there: SQ_VALU_MFMA_BUSY_CYCLES is the same for every variant and
+// GRBM_GUI_ACTIVE follows the time, i.e. the shape sets how much of the MFMA
+// work overlaps the softmax, not how much MFMA work there is.
 //
-// Decode: persistent waves of the stream-K pass.  The decode kernel runs two
-// waves per SIMD, so 2048 waves are one resident round on the 256 CUs of an
-// MI355X; the grid never exceeds the number of 32-key steps a call can have.
+// Decode: persistent waves of the stream-K pass (at most one per 32-key step).
 #pragma once
 
 #include <stdint.h>
