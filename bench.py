@@ -126,6 +126,29 @@ def prefill_bench(seq_len, steps, warmup, batch=8):
     }, case
 
 
+def prefill_bias_variants(steps, warmup, seq_len=4096, batch=8):
+    """The headline shape with the bias from a per-token rel_logits [Tq, Hq, 128]
+    fp32 (what the reference operator takes) and from the fused RelLogitsProj
+    factors r [Tq, Hq, 16] fp32, W [16, 128] (no rel_logits in HBM)."""
+    import torch
+    from inkling_fa4 import (inkling_fa4_rel_attention, inkling_fa4_rel_attention_rproj,
+                             testing)
+
+    case = testing.make_case("per_token", [seq_len] * batch, [seq_len] * batch, 8, 2, 128,
+                             torch.bfloat16, seed=3, rel_table=False)
+    c = case.to("cuda")
+    args = c.args()
+    ms_tok = time_gpu(lambda: inkling_fa4_rel_attention(*args, causal=True,
+                                                        softmax_scale=c.scale), steps, warmup)
+    g = torch.Generator().manual_seed(4)
+    r = (0.3 * torch.randn(case.q.shape[0], 8, 16, generator=g)).to("cuda")
+    w = (0.3 * torch.randn(16, 128, generator=g)).to("cuda")
+    ms_proj = time_gpu(lambda: inkling_fa4_rel_attention_rproj(
+        c.q, c.k, c.v, r, w, c.cu_q, c.cu_k, c.max_q, c.max_k, 128, causal=True,
+        softmax_scale=c.scale), steps, warmup)
+    return {"per_token_rel_ms": ms_tok, "rproj_ms": ms_proj}
+
+
 def decode_bench(steps, warmup, block_size=0, fp8=False):
     """Decode over the 64-sequence batch; block_size > 0: the same keys in a
     paged cache of that block size (blocks in a shuffled physical order);
@@ -360,6 +383,10 @@ def main():
                 sweep[str(s)] = {"ms": round(r["ms"], 5), "tflops": round(r["tflops"], 2),
                                  "frac_of_peak": round(r["frac_of_peak"], 4)}
             result["prefill_sweep"] = sweep
+            bv = prefill_bias_variants(max(5, args.steps // 2), max(2, args.warmup // 2), args.seq)
+            log(f"prefill seq {args.seq}, per-token bias: {bv['per_token_rel_ms']:.4f} ms; "
+                f"fused RelLogitsProj: {bv['rproj_ms']:.4f} ms")
+            result["prefill_bias_variants"] = {k: round(v, 5) for k, v in bv.items()}
     if args.only in ("all", "decode"):
         log(f"decode: {args.steps} steps")
         dec = decode_bench(args.steps, args.warmup)

@@ -107,6 +107,25 @@ typedef struct ifa4_args {
   int32_t rel_dtype;      /* ifa4_dtype */
 } ifa4_args;
 
+/*
+ * Fused relative-logit projection (prefill): instead of a materialised
+ * rel_logits [total_q, n_heads, rel_width], the bias is computed in the kernel
+ * from the low-rank factors of the serving backend's RelLogitsProj
+ * (outputs/architecture.md:24,52-54, einsum(thd,de->the, r, W)):
+ *   bias(token t, head h, dist) = sum_c r[t, h, c] * W[c, dist],  c < d_rel = 16,
+ * applied for 0 <= dist < rel_extent as usual.  r has args.rel_dtype (bf16 or
+ * fp32) and the element strides below (last dim contiguous); W is passed
+ * transposed, wt = W^T [args.rel_width, 16] fp32, rows contiguous.  args.rel and
+ * args.rel_stride_t/h are not read.  rel_extent <= 128 (W^T is staged in LDS).
+ */
+typedef struct ifa4_rel_proj {
+  uint32_t struct_size;   /* sizeof(ifa4_rel_proj) */
+  int32_t d_rel;          /* 16 */
+  const void* r;          /* [total_q, n_heads, d_rel] */
+  int64_t r_stride_t, r_stride_h;
+  const float* wt;        /* [rel_width, d_rel] fp32, 16-byte aligned */
+} ifa4_rel_proj;
+
 /* Tile shape chosen for a call (the gfx950 tile table). */
 typedef struct ifa4_tile {
   int32_t block_q;        /* query rows per workgroup */
@@ -134,6 +153,9 @@ int32_t ifa4_validate(const ifa4_args* args);
  * (NULL = the null stream).
  */
 int32_t ifa4_prefill_fwd(const ifa4_args* args, void* stream);
+
+/* Prefill with the fused relative-logit projection (ifa4_rel_proj). */
+int32_t ifa4_prefill_rproj_fwd(const ifa4_args* args, const ifa4_rel_proj* proj, void* stream);
 
 /* Tile shape ifa4_prefill_fwd uses for these arguments. */
 int32_t ifa4_prefill_tile(const ifa4_args* args, ifa4_tile* tile);

@@ -303,6 +303,40 @@ int32_t ifa4_prefill_fwd(const ifa4_args* args, void* stream) {
   return e == hipSuccess ? IFA4_OK : IFA4_ELAUNCH;
 }
 
+int32_t ifa4_prefill_rproj_fwd(const ifa4_args* args, const ifa4_rel_proj* pr, void* stream) {
+  if (args == nullptr || pr == nullptr || pr->struct_size != sizeof(ifa4_rel_proj))
+    return IFA4_EINVAL;
+  if (pr->d_rel != 16) return IFA4_EUNSUPPORTED;
+  if (args->rel_dtype != IFA4_BF16 && args->rel_dtype != IFA4_FP32) return IFA4_EUNSUPPORTED;
+  if (pr->r_stride_t < 0 || pr->r_stride_h < 0) return IFA4_EINVAL;
+  if (args->rel_extent > 128) return IFA4_EUNSUPPORTED;  // W^T staged in LDS
+  // The rel arguments of ifa4_args describe r here: checked below, not by check_args.
+  ifa4_args b = *args;
+  b.rel = pr->r;
+  b.rel_stride_t = 0;
+  b.rel_stride_h = 0;
+  const int32_t st = check_args(&b);
+  if (st != IFA4_OK) return st;
+  if (args->batch == 0 || args->max_seqlen_q == 0) return IFA4_OK;
+  if (args->rel_extent > 0) {
+    const int64_t esize = args->rel_dtype == IFA4_FP32 ? 4 : 2;
+    if (pr->r == nullptr || pr->wt == nullptr || !aligned(pr->r, esize) || !aligned(pr->wt, 16))
+      return IFA4_EINVAL;
+    if (pr->r_stride_t != 0 && pr->r_stride_t < 16) return IFA4_EUNSUPPORTED;
+    if (((int64_t)args->max_seqlen_q + 128) * pr->r_stride_t * esize >= (int64_t(1) << 31) ||
+        (int64_t)args->rel_width * 64 >= (int64_t(1) << 31))
+      return IFA4_EUNSUPPORTED;
+  }
+  ifa4::PrefillParams p = make_prefill_params(&b);
+  p.rel = pr->r;
+  p.rel_st = pr->r_stride_t;
+  p.rel_sh = pr->r_stride_h;
+  p.wt = args->rel_extent > 0 ? pr->wt : nullptr;  // no bias at all: the plain kernel
+  const hipError_t e = ifa4::launch_prefill(p, args->head_dim, args->qkv_dtype,
+                                            static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IFA4_OK : IFA4_ELAUNCH;
+}
+
 int32_t ifa4_prefill_count_tiles(const ifa4_args* args, const int32_t* cu_q, const int32_t* cu_k,
                                  int64_t* visited, int64_t* total) {
   if (args == nullptr || cu_q == nullptr || cu_k == nullptr || visited == nullptr ||

@@ -30,6 +30,10 @@ struct PrefillParams {
   int32_t n_qtiles;     // ceil(max_seqlen_q / block_q)
   int32_t xcd_pairs;    // (sequence, kv head) pairs per XCD in the XCD-aware order, or 0
   float scale_log2;     // softmax_scale * log2(e)
+  // Fused relative-logit projection (wt != nullptr): rel / rel_st / rel_sh /
+  // rel_dtype describe r [Tq, Hq, 16]; wt is W^T [rel_width, 16] fp32, rows
+  // contiguous; bias(i, dist) = sum_c r[i, c] * wt[dist, c].
+  const float* wt;
 };
 
 struct DecodeParams {

@@ -130,12 +130,27 @@ constexpr int kLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
 constexpr int kBiasPad = 96;
 constexpr int kBiasLdsMax = 1024;  // longest table staged in LDS
 
+// Fused relative-logit projection (kProj): bias(i, dist) = sum_c r[i, c] *
+// W[c, dist] with r [Tq, Hq, kProjDim] and W^T [R', kProjDim] fp32.  The
+// workgroup's 128 rows of r (fp32) and the W^T rows of rel_extent <= kWtLdsMax
+// distances are staged in LDS (8 KiB each: with the two 32 KiB K/V stages
+// exactly 80 KiB, two workgroups per CU); 16-byte chunks of row d are swizzled
+// by (d >> 2) & 3 so that 16 lanes reading 16 consecutive rows hit all 64 banks
+// once.  (A W^T read from L2 for longer extents needed ~100 more VGPRs.)
+constexpr int kProjDim = 16;
+constexpr int kWtLdsMax = 128;
+constexpr int kBiasLdsFloats = 2 * kBiasPad + kBiasLdsMax;           // 1216
+constexpr int kWtLdsFloats = kWtLdsMax * kProjDim;                   // 2048
+__device__ __forceinline__ int wt_lds_index(int d, int chunk) {
+  return d * kProjDim + 4 * (chunk ^ ((d >> 2) & 3));
+}
+
 // Bytes a resource over `rows` rows of `stride` elements (row length d) spans.
 __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int d, int esize) {
   return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + d) * esize) : 0u;
 }
 
-template <int D, typename Tag, typename Rel>
+template <int D, typename Tag, typename Rel, bool kProj>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd,
                                                                           kWavesPerSimd)))
 void prefill_fwd_kernel(PrefillParams p) {
@@ -148,7 +163,9 @@ void prefill_fwd_kernel(PrefillParams p) {
   // constant, which folds into the instruction's offset (one address register
   // per fragment instead of one per fragment and stage).
   __shared__ __align__(1024) uint16_t stages[2 * St::kElems];
-  __shared__ float bias_lds[2 * kBiasPad + kBiasLdsMax];
+  // bias table (shared-table layout) or, with kProj, the W^T rows and r rows
+  __shared__ __align__(16) float bias_lds[kProj ? kWtLdsFloats : kBiasLdsFloats];
+  __shared__ __align__(16) float r_lds[kProj ? kBlockQ * kProjDim : 4];
   uint16_t* const stage0 = stages;
   uint16_t* const stage1 = stages + St::kElems;
 
@@ -308,13 +325,50 @@ void prefill_fwd_kernel(PrefillParams p) {
   };
 #endif
 
-  // Bias resource: the (sequence, head) rows of the bias; each lane reads its rows.
+  // Bias resource: the (sequence, head) rows of the bias (with kProj: of r,
+  // 16 values per row); each lane reads its rows.
   const rsrc_t rrel = make_rsrc(
       static_cast<const char*>(p.rel) + ((int64_t)qs * p.rel_st + (int64_t)head * p.rel_sh) *
                                             Rel::kBytes,
-      span_bytes(lq, p.rel_st, p.rel_width, Rel::kBytes));
+      span_bytes(lq, p.rel_st, kProj ? kProjDim : p.rel_width, Rel::kBytes));
   // Shared-table layout with a table short enough to stage in LDS.
-  const bool bias_in_lds = IFA4_BIAS_LDS && p.rel_st == 0 && rext > 0 && rext <= kBiasLdsMax;
+  const bool bias_in_lds =
+      !kProj && IFA4_BIAS_LDS && p.rel_st == 0 && rext > 0 && rext <= kBiasLdsMax;
+  // Fused projection: W^T [rel_width, 16] fp32; rel_extent <= kWtLdsMax (host-checked).
+  const bool wt_in_lds = kProj;
+  const rsrc_t rwt = make_rsrc(p.wt, kProj ? (uint32_t)((int64_t)p.rel_width * kProjDim * 4) : 0u);
+  // log2(e) * bias of the 16 distances dbase - kc of a 32-key block for this
+  // lane's row (0 outside [0, rext)): the dot product runs over 4-value chunks
+  // of r so that only one chunk of r and one of W^T are live at a time.
+  auto proj_bias = [&](int dbase, int blk, int row, float* bias) {  // row: within the workgroup
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bias[e] = 0.f;
+    if (wt_in_lds) {
+      // four elements at a time; the scheduling barrier keeps the next group's
+      // reads from being hoisted (register pressure of the edge path)
+#pragma unroll
+      for (int eg = 0; eg < 4; ++eg) {
+#pragma unroll
+        for (int ch = 0; ch < kProjDim / 4; ++ch) {
+          const f32x4_t r4 = *reinterpret_cast<const f32x4_t*>(r_lds + wt_lds_index(row, ch));
+#pragma unroll
+          for (int e = 4 * eg; e < 4 * eg + 4; ++e) {
+            const int dist = dbase - (32 * blk + 8 * (e >> 2) + (e & 3));
+            const int d = (uint32_t)dist < (uint32_t)rext ? dist : 0;
+            const f32x4_t w = *reinterpret_cast<const f32x4_t*>(bias_lds + wt_lds_index(d, ch));
+#pragma unroll
+            for (int c = 0; c < 4; ++c) bias[e] = fmaf(r4[c], w[c], bias[e]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int dist = dbase - (32 * blk + 8 * (e >> 2) + (e & 3));
+      bias[e] = (uint32_t)dist < (uint32_t)rext ? bias[e] * kLog2e : 0.f;
+    }
+  };
 
   // Lane constants of the LDS fragment reads.
   // K (A operand of QK): row 32*blk + col, chunk 2*kk + half.
@@ -393,10 +447,14 @@ void prefill_fwd_kernel(PrefillParams p) {
       return u32x4_t{part[0][0], part[0][1], part[1][0], part[1][1]};
     };
     // Key block 0's V^T fragments are read now; their latency hides behind the
-    // softmax below.
+    // softmax below.  Not on bias tiles of the fused projection, whose bias
+    // computation needs the registers (it is long enough to hide them anyway).
     u32x4_t vfr[kDBlocks];
+    const bool vfr_early = !(kProj && has_bias);
+    if (vfr_early) {
 #pragma unroll
-    for (int db = 0; db < kDBlocks; ++db) vfr[db] = read_vt(db, 0);
+      for (int db = 0; db < kDBlocks; ++db) vfr[db] = read_vt(db, 0);
+    }
 #endif
 
     // ---- logits (log2 domain) and tile max ---------------------------------------
@@ -427,6 +485,8 @@ void prefill_fwd_kernel(PrefillParams p) {
               const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
               bias[e] = tb[kBlockK - 1 - kc];
             }
+          } else if (has_bias && kProj) {
+            proj_bias(dbase, blk, qi[qb] - q0, bias);
           } else if (has_bias) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -462,6 +522,13 @@ void prefill_fwd_kernel(PrefillParams p) {
         mx[qb] = m * c2;
       }
     }
+
+#if IFA4_PV2
+    if (!vfr_early) {
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) vfr[db] = read_vt(db, 0);
+    }
+#endif
 
     // ---- deferred rescale ----------------------------------------------------------
     bool grow[kNqb];
@@ -659,8 +726,46 @@ void prefill_fwd_kernel(PrefillParams p) {
       tab[i] = Rel::load(rrel, off) * kLog2e;
     }
   }
+  // Fused projection: the workgroup's rows of r (fp32) and W^T rows [0, rext)
+  // into LDS (swizzled 16-byte chunks), read with the Q fragments.
+  constexpr int kRPer = kProj ? kBlockQ * kProjDim / 4 / kThreads : 1;  // chunks per thread
+  constexpr int kWtPer = kProj ? kWtLdsFloats / 4 / kThreads : 1;
+  f32x4_t rtab[kRPer], wtab[kWtPer];
+  if constexpr (kProj) {
+#pragma unroll
+    for (int i = 0; i < kRPer; ++i) {
+      const int idx = tid + i * kThreads;  // row idx / 4 of the workgroup, chunk idx % 4
+      const uint32_t off =
+          (uint32_t)((int64_t)(q0 + (idx >> 2)) * p.rel_st + 4 * (idx & 3)) * Rel::kBytes;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) rtab[i][c] = Rel::load(rrel, off + c * Rel::kBytes);
+    }
+    if (wt_in_lds) {
+#pragma unroll
+      for (int i = 0; i < kWtPer; ++i) {
+        const int idx = tid + i * kThreads;  // W^T row idx / 4, chunk idx % 4
+        const uint32_t off = (idx >> 2) < rext ? (uint32_t)idx * 16 : kOutOfRange;
+        wtab[i] = __builtin_bit_cast(f32x4_t, buf_load_16(rwt, off));
+      }
+    }
+  }
   if (kt_beg < kt_end) dma_tile(kt_beg, stage0);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if constexpr (kProj) {
+#pragma unroll
+    for (int i = 0; i < kRPer; ++i) {
+      const int idx = tid + i * kThreads;
+      *reinterpret_cast<f32x4_t*>(r_lds + wt_lds_index(idx >> 2, idx & 3)) = rtab[i];
+    }
+    if (wt_in_lds) {
+#pragma unroll
+      for (int i = 0; i < kWtPer; ++i) {
+        const int idx = tid + i * kThreads;
+        *reinterpret_cast<f32x4_t*>(bias_lds + wt_lds_index(idx >> 2, idx & 3)) = wtab[i];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+  }
   if (bias_in_lds) {
 #pragma unroll
     for (int i = 0; i < kBiasPer; ++i) {
@@ -700,7 +805,7 @@ void prefill_fwd_kernel(PrefillParams p) {
   }
 }
 
-template <int D, typename Tag, typename Rel>
+template <int D, typename Tag, typename Rel, bool kProj>
 hipError_t launch_prefill_t(const PrefillParams& p_in, hipStream_t stream) {
   PrefillParams p = p_in;
   const int per_tile = p.n_heads * p.batch;
@@ -708,17 +813,21 @@ hipError_t launch_prefill_t(const PrefillParams& p_in, hipStream_t stream) {
   const int pairs = p.batch * (p.n_heads / p.group);
   p.xcd_pairs = pairs % 8 == 0 ? pairs / 8 : 0;
   if (blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL((prefill_fwd_kernel<D, Tag, Rel>), dim3((unsigned)blocks), dim3(kThreads),
-                     0, stream, p);
+  hipLaunchKernelGGL((prefill_fwd_kernel<D, Tag, Rel, kProj>), dim3((unsigned)blocks),
+                     dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 
 template <int D, typename Tag>
 hipError_t launch_prefill_rel(const PrefillParams& p, hipStream_t stream) {
+  if (p.wt != nullptr) {  // fused projection: r in bf16 or fp32
+    return p.rel_dtype == 2 ? launch_prefill_t<D, Tag, RelF32, true>(p, stream)
+                            : launch_prefill_t<D, Tag, RelBf16, true>(p, stream);
+  }
   switch (p.rel_dtype) {
-    case 0: return launch_prefill_t<D, Tag, RelBf16>(p, stream);
-    case 1: return launch_prefill_t<D, Tag, RelF16>(p, stream);
-    default: return launch_prefill_t<D, Tag, RelF32>(p, stream);
+    case 0: return launch_prefill_t<D, Tag, RelBf16, false>(p, stream);
+    case 1: return launch_prefill_t<D, Tag, RelF16, false>(p, stream);
+    default: return launch_prefill_t<D, Tag, RelF32, false>(p, stream);
   }
 }
 

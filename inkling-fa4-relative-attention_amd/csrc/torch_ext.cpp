@@ -1,6 +1,6 @@
 // Thin PyTorch-ROCm binding over the C ABI (include/ifa4.h).
 //
-// Registers torch.ops.inkling_fa4.fwd / .decode / .decode_paged.  The binding checks tensor
+// Registers torch.ops.inkling_fa4.fwd / .fwd_rproj / .decode / .decode_paged.  The binding checks tensor
 // devices, dtypes and shapes, allocates out / lse / the decode workspace from
 // torch's caching allocator, fills an ifa4_args and calls the library on the
 // current HIP stream.  No math happens here, and there is no fallback: a
@@ -137,6 +137,50 @@ std::tuple<at::Tensor, at::Tensor> fwd(const at::Tensor& q, const at::Tensor& k,
   return {out, lse};
 }
 
+// Prefill with the fused relative-logit projection: r [Tq, Hq, 16] (bf16 or
+// fp32), wt = W^T [R', 16] fp32 contiguous.
+std::tuple<at::Tensor, at::Tensor> fwd_rproj(const at::Tensor& q, const at::Tensor& k,
+                                             const at::Tensor& v, const at::Tensor& r,
+                                             const at::Tensor& wt, const at::Tensor& cu_q,
+                                             const at::Tensor& cu_k, int64_t max_q, int64_t max_k,
+                                             int64_t rel_extent, bool causal, int64_t window_left,
+                                             double softmax_scale, bool return_lse,
+                                             int64_t flags) {
+  TORCH_CHECK(r.dim() == 3 && r.size(0) == q.size(0) && r.size(1) == q.size(1) &&
+                  r.size(2) == 16 && r.stride(2) == 1,
+              "inkling_fa4.fwd_rproj: r must be [total_q, n_heads, 16] with a contiguous last dim");
+  TORCH_CHECK(wt.dim() == 2 && wt.size(1) == 16 && wt.is_contiguous() &&
+                  wt.scalar_type() == at::kFloat,
+              "inkling_fa4.fwd_rproj: wt must be W^T [R', 16] fp32, contiguous");
+  TORCH_CHECK(r.scalar_type() == at::kFloat || r.scalar_type() == at::kBFloat16,
+              "inkling_fa4.fwd_rproj: r must be fp32 or bf16");
+  TORCH_CHECK(wt.is_cuda() && wt.device() == q.device(), "inkling_fa4.fwd_rproj: wt on q's GPU");
+  // make_args checks r in the rel slot: a [total_q, n_heads, 16] view passes
+  ifa4_args a = make_args(q, k, v, r, cu_q, cu_k, max_q, max_k, rel_extent, causal, window_left,
+                          softmax_scale, flags);
+  a.rel_width = static_cast<int32_t>(wt.size(0));
+  ifa4_rel_proj pr{};
+  pr.struct_size = sizeof(ifa4_rel_proj);
+  pr.d_rel = 16;
+  pr.r = r.data_ptr();
+  pr.r_stride_t = r.stride(0);
+  pr.r_stride_h = r.stride(1);
+  pr.wt = wt.data_ptr<float>();
+  at::Tensor out = at::empty_like(q, q.options().memory_format(at::MemoryFormat::Contiguous));
+  at::Tensor lse = return_lse ? at::empty({q.size(1), q.size(0)}, q.options().dtype(at::kFloat))
+                              : at::empty({0}, q.options().dtype(at::kFloat));
+  a.out = out.data_ptr();
+  a.out_stride_t = out.stride(0);
+  a.out_stride_h = out.stride(1);
+  if (return_lse) {
+    a.lse = lse.data_ptr<float>();
+    a.lse_stride_h = lse.stride(0);
+  }
+  const hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
+  check_status(ifa4_prefill_rproj_fwd(&a, &pr, stream), "fwd_rproj");
+  return {out, lse};
+}
+
 std::tuple<at::Tensor, at::Tensor> decode(const at::Tensor& q, const at::Tensor& k,
                                           const at::Tensor& v, const at::Tensor& rel,
                                           const at::Tensor& cu_q, const at::Tensor& cu_k,
@@ -257,6 +301,10 @@ TORCH_LIBRARY(inkling_fa4, m) {
       "Tensor cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, int rel_extent, bool causal, "
       "int window_left, float softmax_scale, bool return_lse, int flags) -> (Tensor, Tensor)");
   m.def(
+      "fwd_rproj(Tensor q, Tensor k, Tensor v, Tensor r, Tensor wt, Tensor cu_seqlens_q, "
+      "Tensor cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, int rel_extent, bool causal, "
+      "int window_left, float softmax_scale, bool return_lse, int flags) -> (Tensor, Tensor)");
+  m.def(
       "decode(Tensor q, Tensor k, Tensor v, Tensor rel_logits, Tensor cu_seqlens_q, "
       "Tensor cu_seqlens_k, int max_seqlen_q, int max_seqlen_k, int rel_extent, bool causal, "
       "int window_left, float softmax_scale, bool return_lse, int flags, float k_scale, "
@@ -270,6 +318,7 @@ TORCH_LIBRARY(inkling_fa4, m) {
 
 TORCH_LIBRARY_IMPL(inkling_fa4, CUDA, m) {
   m.impl("fwd", &fwd);
+  m.impl("fwd_rproj", &fwd_rproj);
   m.impl("decode", &decode);
   m.impl("decode_paged", &decode_paged);
 }

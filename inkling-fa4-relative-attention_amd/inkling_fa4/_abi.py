@@ -74,6 +74,11 @@ class Ifa4KvQuant(ctypes.Structure):
                 ("k_scale", ctypes.c_float), ("v_scale", ctypes.c_float)]
 
 
+class Ifa4RelProj(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("d_rel", _c_int32), ("r", _vp),
+                ("r_stride_t", _c_int64), ("r_stride_h", _c_int64), ("wt", _vp)]
+
+
 _P_ARGS = ctypes.POINTER(Ifa4Args)
 _P_PAGED = ctypes.POINTER(Ifa4PagedKV)
 _P_QUANT = ctypes.POINTER(Ifa4KvQuant)
@@ -87,6 +92,7 @@ SIGNATURES = {
     "ifa4_validate": (_c_int32, [_P_ARGS]),
     "ifa4_prefill_fwd": (_c_int32, [_P_ARGS, _vp]),
     "ifa4_prefill_tile": (_c_int32, [_P_ARGS, _P_TILE]),
+    "ifa4_prefill_rproj_fwd": (_c_int32, [_P_ARGS, ctypes.POINTER(Ifa4RelProj), _vp]),
     "ifa4_prefill_count_tiles": (_c_int32, [_P_ARGS, _P_I32, _P_I32, _P_I64, _P_I64]),
     "ifa4_decode_workspace_bytes": (ctypes.c_size_t, [_P_ARGS]),
     "ifa4_decode_tile": (_c_int32, [_P_ARGS, _P_TILE]),

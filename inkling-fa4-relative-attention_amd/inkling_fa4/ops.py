@@ -9,7 +9,9 @@ signatures:
 
 plus the same entry points under names without the `_triton` suffix, and
 `inkling_fa4_rel_attention_decode_paged` for a paged KV cache (block tables),
-the format of the serving caller (outputs/architecture.md:117-120).
+the format of the serving caller (outputs/architecture.md:117-120), and
+`inkling_fa4_rel_attention_rproj` with the bias computed in the kernel from the
+RelLogitsProj factors (outputs/architecture.md:24,52-54).
 
 Differences from the reference wrappers (all deliberate):
   * one kernel launch for the whole batch and no host synchronisation (the
@@ -152,6 +154,31 @@ def inkling_fa4_rel_attention_decode_paged(q, k_cache, v_cache, rel_logits, cu_s
                                    int(rel_extent), bool(causal), _window_left(window_size),
                                    scale, bool(return_lse), _flag_bits(bottom_right),
                                    float(k_scale), float(v_scale))
+    return (out, lse) if return_lse else out
+
+
+@torch.no_grad()
+def inkling_fa4_rel_attention_rproj(q, k, v, rel_r, rel_w, cu_seqlens_q, cu_seqlens_k,
+                                    max_seqlen_q, max_seqlen_k, rel_extent, causal=True,
+                                    window_size=(-1, -1), *, softmax_scale=None,
+                                    return_lse=False, bottom_right=False):
+    """Prefill with the relative bias computed in the kernel from the low-rank
+    factors of the serving backend's RelLogitsProj (outputs/architecture.md:24,
+    52-54): rel_logits = einsum('thd,de->the', rel_r, rel_w) is never
+    materialised.
+
+    rel_r [total_q, Hq, 16] (bf16 or fp32, last dim contiguous), rel_w [16, R']
+    with R' >= rel_extent and rel_extent <= 128.  Otherwise as
+    inkling_fa4_rel_attention.
+    """
+    scale = _resolve(q, k, None, None, None, softmax_scale)
+    if rel_w.dim() != 2 or rel_w.shape[0] != rel_r.shape[-1]:
+        raise ValueError("rel_w must be [d_rel, R'] with d_rel = rel_r.shape[-1]")
+    wt = rel_w.t().to(torch.float32).contiguous()  # W^T [R', 16], 64 bytes per distance
+    out, lse = _ops().fwd_rproj(q, k, v, rel_r, wt, cu_seqlens_q, cu_seqlens_k,
+                                int(max_seqlen_q), int(max_seqlen_k), int(rel_extent),
+                                bool(causal), _window_left(window_size), scale, bool(return_lse),
+                                _flag_bits(bottom_right))
     return (out, lse) if return_lse else out
 
 

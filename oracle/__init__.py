@@ -11,6 +11,8 @@ Contents
                  log-sum-exp the reference does not return.
   merge.py       closed-form log-sum-exp merge of split partials (the
                  split-KV decode combine; no reference counterpart).
+  rproj.py       relative logits from the RelLogitsProj factors (fp32 einsum),
+                 then the oracle (no kernel counterpart in the reference).
   paged.py       paged KV cache (block tables) -> contiguous varlen K/V, and
                  the oracle over a paged cache (the serving format of
                  outputs/architecture.md:117-120; no kernel counterpart in
@@ -28,6 +30,8 @@ How each function is pinned (see tests/test_oracle_*.py):
                  library routine) and sum_j exp(s_ij - lse_i) == 1.
   merge_partials split-count invariance (1, 2, 7 and one split per key) and
                  equality with the unsplit oracle.
+  rel_logits_from_proj  an explicit loop on a tiny shape; a rank-one W that
+                 reproduces a per-head table.
   gather_paged   identity tables reproduce the contiguous cache; invariance
                  under physical block permutation and block size; rows no
                  sequence owns (NaN-filled) never reach the result.
@@ -35,3 +39,4 @@ How each function is pinned (see tests/test_oracle_*.py):
 from .reference import ref_rel_attn, ref_rel_attn_with_lse  # noqa: F401
 from .merge import merge_partials  # noqa: F401
 from .paged import gather_paged, ref_rel_attn_paged_with_lse  # noqa: F401
+from .rproj import ref_rel_attn_rproj_with_lse, rel_logits_from_proj  # noqa: F401
