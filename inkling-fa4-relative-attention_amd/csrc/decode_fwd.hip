@@ -40,10 +40,25 @@
 #include "ifa4_device.hpp"
 #include "ifa4_kernels.h"
 
+#ifndef IFA4_DECODE_NT
+#define IFA4_DECODE_NT 1
+#endif
+
 namespace ifa4 {
 namespace {
 
 constexpr int kStep = 32;  // keys per pipeline step of a decode wave
+
+// K/V stream loads.  Each cache byte is read once per call, so the loads are
+// marked non-temporal: a streaming-read probe over the 580 MB benchmark cache
+// measured 6.2-6.6 TB/s with non-temporal loads against 5.7 TB/s without.
+__device__ __forceinline__ u32x4_t kv_load(rsrc_t r, uint32_t byte_off) {
+#if IFA4_DECODE_NT
+  return buf_load_16_nt(r, byte_off);
+#else
+  return buf_load_16(r, byte_off);
+#endif
+}
 constexpr int kDecodeFp8MaxGroup = 8;
 
 // Lane layouts of a decode wave (D = head_dim, Eb = bytes per K/V element):
@@ -286,8 +301,8 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
       const uint32_t row = (uint32_t)(key & bmask);
       const bool valid = key < cu.kend;
       const int grp = (S::kRpi * i) / S::kGroupRows;
-      kr[i] = buf_load_16(rk[grp], valid ? row * k_row + 16 * c : kOutOfRange);
-      vr[i] = buf_load_16(rv[grp], valid ? row * v_row + 16 * c : kOutOfRange);
+      kr[i] = kv_load(rk[grp], valid ? row * k_row + 16 * c : kOutOfRange);
+      vr[i] = kv_load(rv[grp], valid ? row * v_row + 16 * c : kOutOfRange);
     }
   };
   auto load = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu) {
@@ -304,8 +319,8 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
 #pragma unroll
       for (int i = 0; i < S::kLoads; ++i) {
         const uint32_t row = (uint32_t)(k0 + S::kRpi * i + r);
-        kr[i] = buf_load_16(rk, row * k_row + 16 * c);
-        vr[i] = buf_load_16(rv, row * v_row + 16 * c);
+        kr[i] = kv_load(rk, row * k_row + 16 * c);
+        vr[i] = kv_load(rv, row * v_row + 16 * c);
       }
     }
   };

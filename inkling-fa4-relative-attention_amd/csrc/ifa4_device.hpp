@@ -167,6 +167,10 @@ __device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, uint32_t b
 __device__ __forceinline__ u32x4_t buf_load_16(rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0));
 }
+// Same, marked non-temporal (streamed once; not kept in the caches).
+__device__ __forceinline__ u32x4_t buf_load_16_nt(rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 2));
+}
 __device__ __forceinline__ uint32_t buf_load_4(rsrc_t r, uint32_t byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0);
 }

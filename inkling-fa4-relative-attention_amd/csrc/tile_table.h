@@ -36,7 +36,9 @@ constexpr PrefillTileEntry kPrefillTiles[] = {
 
 // Persistent waves of the decode stream pass (at most; never more than the
 // steps), from the sweep on the 64-sequence batch (KV 1K-16K, non-causal;
-// profiles/sweep_decode_waves_b64.md):
+// profiles/sweep_decode_waves_b64.md, before the K/V loads were non-temporal;
+// with them, profiles/sweep_decode_nt_b64.md: contiguous 896 waves 0.097 ms,
+// 1536 0.103; paged 0.105 either way):
 //   contiguous bf16: 896 waves 0.112 ms, 1024 0.112, 768 0.113, 2048 0.116,
 //                    512 0.151 (too few bytes in flight);
 //   paged (blocks of 16): 2048 0.120, 1024 0.121, 896 0.133, 768 0.149 -- a
