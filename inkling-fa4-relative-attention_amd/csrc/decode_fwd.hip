@@ -20,9 +20,9 @@
 // split needs no host synchronisation and no atomics.
 //
 // Pass 1 (decode_stream_kernel), per 32-key step of a segment:
-//   * K and V rows arrive with coalesced 16-byte buffer loads one step ahead
-//     of the compute (register double buffering), rows past the segment end
-//     read as zero; the next segment's Q (all G query heads of the kv head)
+//   * K and V rows arrive with coalesced, non-temporal 16-byte buffer loads one
+//     step ahead of the compute (register double buffering), rows past the
+//     segment end read as zero; the next segment's Q (all G query heads of the kv head)
 //     arrives ahead of it by LDS DMA into a two-slot ring;
 //   * K goes through a small padded LDS tile into the A operand of
 //     S^T = K Q^T on v_mfma_f32_16x16x32 (B = the G query rows, zero padded to
