@@ -43,8 +43,12 @@ int32_t check_args(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr, int kv
     return IFA4_EINVAL;
   if (!(std::isfinite(a->softmax_scale))) return IFA4_EINVAL;
   if (a->batch == 0) return IFA4_OK;  // nothing to read or write
-  if (a->q == nullptr || a->k == nullptr || a->v == nullptr || a->out == nullptr ||
-      a->cu_seqlens_q == nullptr || (kv == nullptr && a->cu_seqlens_k == nullptr))
+  if (a->cu_seqlens_q == nullptr || (kv == nullptr && a->cu_seqlens_k == nullptr))
+    return IFA4_EINVAL;
+  // Empty query or key sets may come with null data pointers (an empty tensor's
+  // storage); the kernels then read nothing from them.
+  if ((a->q == nullptr || a->out == nullptr) && a->total_q > 0) return IFA4_EINVAL;
+  if ((a->k == nullptr || a->v == nullptr) && (kv != nullptr || a->total_k > 0))
     return IFA4_EINVAL;
   if (a->rel_extent > 0 && a->rel == nullptr) return IFA4_EINVAL;
   if (a->lse != nullptr) {

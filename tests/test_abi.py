@@ -81,6 +81,10 @@ def _validate(**kw):
     ({"qkv_dtype": _abi.IFA4_FP16, "rel_dtype": _abi.IFA4_BF16}, _abi.IFA4_OK),
     ({"batch": 0, "q": 0, "k": 0}, _abi.IFA4_OK),  # empty batch: nothing is touched
     ({"q": 0}, _abi.IFA4_EINVAL),
+    ({"k": 0}, _abi.IFA4_EINVAL),
+    # no keys at all: K/V may be null (an empty tensor's storage), nothing is read
+    ({"k": 0, "v": 0, "total_k": 0, "max_seqlen_k": 0}, _abi.IFA4_OK),
+    ({"q": 0, "out": 0, "total_q": 0, "max_seqlen_q": 0}, _abi.IFA4_OK),
     ({"cu_seqlens_k": 0}, _abi.IFA4_EINVAL),
     ({"rel": 0}, _abi.IFA4_EINVAL),
     ({"rel": 0, "rel_extent": 0}, _abi.IFA4_OK),  # no bias at all

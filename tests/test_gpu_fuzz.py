@@ -1,0 +1,86 @@
+"""Seeded random sweep of the prefill and decode entry points against the oracle.
+
+Each case draws its own shapes and options (ragged lengths with Lk >= Lq and
+Lk < Lq, GQA ratios, head_dim 64/128, bf16/fp16, causal or not, left windows,
+rel_extent from 1 to past the table width of the shared layout, per-token and
+shared bias, bf16/fp32 bias, top-left and bottom-right alignment), runs the
+HIP path and compares every row with the fp32 oracle at the operator's
+tolerances (out atol/rtol 2e-2, lse atol 1e-3).
+"""
+import random
+
+import pytest
+import torch
+
+from inkling_fa4 import inkling_fa4_rel_attention, inkling_fa4_rel_attention_decode, testing
+from oracle import ref_rel_attn_with_lse
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL, LSE_ATOL = 2e-2, 2e-2, 1e-3
+HEADS = [(4, 4), (8, 2), (6, 3), (8, 1), (2, 1), (16, 4)]
+
+
+def _draw(seed, decode):
+    r = random.Random(seed)
+    batch = r.randint(1, 6)
+    if decode:
+        lens_q = [1] * batch
+        lens_k = [r.choice([0, 1, r.randint(1, 64), r.randint(64, 1500)]) for _ in range(batch)]
+    else:
+        lens_q = [r.choice([1, r.randint(1, 64), r.randint(64, 300)]) for _ in range(batch)]
+        lens_k = [max(0, lq + r.choice([0, r.randint(0, 300), -r.randint(0, lq)])) for lq in lens_q]
+    hq, hkv = r.choice(HEADS)
+    head_dim = r.choice([64, 128])
+    dtype = r.choice([torch.bfloat16, torch.float16])
+    rel_extent = r.choice([1, 16, 100, 128, 200])
+    opts = dict(
+        causal=r.random() < 0.6,
+        window_left=r.choice([-1, -1, 0, r.randint(1, 200)]),
+        rel_table=r.random() < 0.6,
+        rel_dtype=r.choice([torch.float32, torch.bfloat16]),
+        rel_extent=rel_extent,
+        rel_width=rel_extent + r.choice([0, 0, 7]),
+        scale=r.choice([None, 0.3]),
+    )
+    bottom_right = r.random() < 0.3
+    return lens_q, lens_k, hq, hkv, head_dim, dtype, opts, bottom_right
+
+
+def _check(case, out, lse, bottom_right):
+    """Rows that see no key are NaN in the oracle (the reference's softmax over
+    nothing); the operator writes out = 0 and lse = -inf there."""
+    want_out, want_lse = ref_rel_attn_with_lse(
+        case.q, case.k, case.v, case.rel, case.cu_q, case.cu_k, case.scale, case.rel_extent,
+        causal=case.causal, window_left=case.window_or_none, bottom_right=bottom_right)
+    out, lse = out.cpu().float(), lse.cpu().transpose(0, 1)  # lse as [Tq, Hq]
+    want_lse = want_lse.transpose(0, 1)
+    empty = torch.isnan(want_out.float()).any(-1) | torch.isneginf(want_lse)  # [Tq, Hq]
+    assert (out[empty] == 0).all()
+    assert torch.isneginf(lse[empty]).all()
+    keep = ~empty
+    torch.testing.assert_close(out[keep], want_out.float()[keep], atol=ATOL, rtol=RTOL)
+    torch.testing.assert_close(lse[keep], want_lse[keep], atol=LSE_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_prefill_random_configs(cuda, seed):
+    lens_q, lens_k, hq, hkv, d, dtype, opts, br = _draw(1000 + seed, decode=False)
+    case = testing.make_case(f"fuzz{seed}", lens_q, lens_k, hq, hkv, d, dtype, seed=seed, **opts)
+    c = case.to(cuda)
+    out, lse = inkling_fa4_rel_attention(*c.args(), causal=c.causal, window_size=c.window_size,
+                                         softmax_scale=c.scale, return_lse=True, bottom_right=br)
+    torch.cuda.synchronize()
+    _check(case, out, lse, br)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_decode_random_configs(cuda, seed):
+    lens_q, lens_k, hq, hkv, d, dtype, opts, br = _draw(2000 + seed, decode=True)
+    case = testing.make_case(f"fuzzd{seed}", lens_q, lens_k, hq, hkv, d, dtype, seed=seed, **opts)
+    c = case.to(cuda)
+    out, lse = inkling_fa4_rel_attention_decode(*c.args(), causal=c.causal,
+                                                window_size=c.window_size, softmax_scale=c.scale,
+                                                return_lse=True, bottom_right=br)
+    torch.cuda.synchronize()
+    _check(case, out, lse, br)
