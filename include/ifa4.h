@@ -71,6 +71,8 @@ typedef enum ifa4_dtype {
  *   cu_seqlens_q/k: device int32 [batch+1], non-decreasing, cu[0] = 0,
  *        cu_q[batch] <= total_q, cu_k[batch] <= total_k.  Read only on the device.
  * max_seqlen_q/k must bound every sequence length; they size the grid.
+ * q and out may be NULL when total_q == 0, k and v when total_k == 0 (contiguous
+ * K/V): nothing is read from or written to them then.
  * Mirrors the argument list of inkling_fa4_rel_attention_triton
  * (src/inkling_fa4/triton_kernel.py:85-89,99-105) plus softmax_scale and lse.
  */
