@@ -47,9 +47,11 @@ def test_decode_fp16(cuda):
     _check(_decode(case, cuda), _oracle(case))
 
 
-@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (12, 4), (8, 1), (16, 1), (6, 2)])
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 2), (12, 4), (8, 1), (16, 1), (6, 2), (32, 1),
+                                     (48, 2)])
 @pytest.mark.parametrize("head_dim", [64, 128])
 def test_decode_gqa_groups_and_head_dims(cuda, hq, hkv, head_dim):
+    """Groups above 16 (32, 24) run through the prefill kernel."""
     lens = [1, 2, 63, 64, 65, 200, 1000, 3000]
     case = testing.make_case("dec_gqa", [1] * len(lens), lens, hq, hkv, head_dim, torch.bfloat16,
                              seed=hq * 10 + hkv, causal=False, rel_table=False, scale=0.1)
