@@ -109,6 +109,31 @@ def test_validate(kw, expect):
     assert _validate(**kw) == expect
 
 
+def _first_len_at_limit(stride_bytes, extra_bytes=0):
+    """Smallest length L with (L + 128) * stride_bytes + extra_bytes >= 2 GiB."""
+    return -(-((1 << 31) - extra_bytes) // stride_bytes) - 128
+
+
+def test_validate_span_limits():
+    """A sequence (plus the 128 rows a tile may read past its end) must span
+    less than 2 GiB of K, V, Q and per-token bias: the kernels address it
+    through a buffer resource with 32-bit offsets.  Checked one step on each
+    side of the limit."""
+    lk = _first_len_at_limit(2 * 128 * 2)  # k_stride_t = 256 bf16
+    ok = dict(max_seqlen_k=lk - 1, total_k=2 * lk)
+    assert _validate(**ok) == _abi.IFA4_OK
+    assert _validate(**dict(ok, max_seqlen_k=lk)) == _abi.IFA4_EUNSUPPORTED
+    lq = _first_len_at_limit(8 * 128 * 2)  # q_stride_t = 1024 bf16
+    ok = dict(max_seqlen_q=lq - 1, total_q=2 * lq)
+    assert _validate(**ok) == _abi.IFA4_OK
+    assert _validate(**dict(ok, max_seqlen_q=lq)) == _abi.IFA4_EUNSUPPORTED
+    # per-token fp32 bias rows of 8 * 128 floats (rel_stride_t = 1024)
+    lr = _first_len_at_limit(1024 * 4, extra_bytes=128 * 4)
+    ok = dict(max_seqlen_q=lr - 1, total_q=2 * lr, rel_stride_t=1024)
+    assert _validate(**ok) == _abi.IFA4_OK
+    assert _validate(**dict(ok, max_seqlen_q=lr)) == _abi.IFA4_EUNSUPPORTED
+
+
 def test_launch_entry_points_reject_bad_args_before_any_launch():
     lib = _abi.lib()
     bad = _good(head_dim=96)
