@@ -85,9 +85,15 @@ namespace {
 constexpr int kNqb = IFA4_PREFILL_NQB;           // 32-row query blocks per wave
 constexpr int kWaves = kNqb == 1 ? 4 : 2;        // waves per workgroup
 constexpr int kBlockQ = 32 * kNqb * kWaves;      // 128
-constexpr int kBlockK = 64;
+#ifndef IFA4_BLOCK_K
+#define IFA4_BLOCK_K 64
+#endif
+constexpr int kBlockK = IFA4_BLOCK_K;            // keys per KV tile (32 or 64)
 constexpr int kThreads = 64 * kWaves;
-constexpr int kWavesPerSimd = kNqb == 1 ? 2 : 1;
+#ifndef IFA4_WPE
+#define IFA4_WPE (kNqb == 1 ? 2 : 1)
+#endif
+constexpr int kWavesPerSimd = IFA4_WPE;         // occupancy the register budget targets
 #ifndef IFA4_LOOK_K
 #define IFA4_LOOK_K 4
 #endif

@@ -26,6 +26,8 @@ Knobs (macros of the kernel sources):
                    IFA4_PV2                   key-block-major PV (0/1)
                    IFA4_BIAS_LDS              shared bias table in LDS (0/1)
                    IFA4_PREFILL_NQB           32-row blocks per wave (1/2)
+                   IFA4_BLOCK_K               keys per KV tile (32/64)
+                   IFA4_WPE                   waves per SIMD the register budget targets
   tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
                    IFA4_DECODE_WAVES_FP8      the same for an fp8 KV cache (workload decode_fp8)
 """
