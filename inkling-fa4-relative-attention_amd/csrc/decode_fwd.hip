@@ -43,6 +43,9 @@
 #ifndef IFA4_DECODE_NT
 #define IFA4_DECODE_NT 1
 #endif
+#ifndef IFA4_FP8_CVT2
+#define IFA4_FP8_CVT2 1
+#endif
 
 namespace ifa4 {
 namespace {
@@ -372,11 +375,19 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
         // fp8 -> the MFMA type (exact); the K scale is folded into the logit scale
 #pragma unroll
         for (int hlf = 0; hlf < 2; ++hlf) {
+#if IFA4_FP8_CVT2
+          // one conversion per pair, straight to the 16-bit type
+          const uint32_t w0 = kr[i][2 * hlf], w1 = kr[i][2 * hlf + 1];
+          *reinterpret_cast<u32x4_t*>(dst + 8 * hlf) =
+              u32x4_t{E::template fp8x2<false>(w0), E::template fp8x2<true>(w0),
+                      E::template fp8x2<false>(w1), E::template fp8x2<true>(w1)};
+#else
           float f[8];
           fp8x8_to_f32(kr[i][2 * hlf], kr[i][2 * hlf + 1], f);
           *reinterpret_cast<u32x4_t*>(dst + 8 * hlf) =
               u32x4_t{E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]),
                       E::pack2(f[6], f[7])};
+#endif
         }
       }
     }

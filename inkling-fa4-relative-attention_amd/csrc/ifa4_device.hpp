@@ -51,6 +51,12 @@ template <> struct Elem<Bf16Tag> {
     const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), one, acc, false);
   }
+  // OCP e4m3 bytes 2*HI, 2*HI+1 of w -> packed pair, one conversion, exact
+  // (scale 1; every e4m3 value is a bf16 value).
+  template <bool HI>
+  static __device__ __forceinline__ uint32_t fp8x2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+  }
   static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
   static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
   static __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
@@ -72,6 +78,11 @@ template <> struct Elem<F16Tag> {
     typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
     const f16x2_t one = {(_Float16)1.0f, (_Float16)1.0f};
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), one, acc, false);
+  }
+  // OCP e4m3 bytes 2*HI, 2*HI+1 of w -> packed pair, exact (e4m3 fits fp16).
+  template <bool HI>
+  static __device__ __forceinline__ uint32_t fp8x2(uint32_t w) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
   }
   static __device__ __forceinline__ float lo(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
