@@ -69,8 +69,13 @@ typedef enum ifa4_dtype {
  *   out [total_q, n_heads,  head_dim]   qkv_dtype
  *   lse [n_heads, total_q] fp32 with head stride lse_stride_h (may be NULL)
  *   cu_seqlens_q/k: device int32 [batch+1], non-decreasing, cu[0] = 0,
- *        cu_q[batch] <= total_q, cu_k[batch] <= total_k.  Read only on the device.
- * max_seqlen_q/k must bound every sequence length; they size the grid.
+ *        cu_q[batch] <= total_q, cu_k[batch] <= total_k.  Read only on the device,
+ *        where each sequence's [cu[b], cu[b+1]) is clamped to [0, total]: offsets
+ *        outside that range, or decreasing, give shorter or empty sequences
+ *        (results for them are unspecified) but never reads or writes outside
+ *        the tensors.
+ * max_seqlen_q/k must bound every sequence length; they size the grid (query
+ * rows past max_seqlen_q are not written).
  * q and out may be NULL when total_q == 0, k and v when total_k == 0 (contiguous
  * K/V): nothing is read from or written to them then.
  * Mirrors the argument list of inkling_fa4_rel_attention_triton
@@ -172,7 +177,9 @@ int32_t ifa4_prefill_count_tiles(const ifa4_args* args, const int32_t* host_cu_s
                                  int64_t* total);
 
 /*
- * Decode: exactly one query token per sequence (total_q == batch).  Split-KV,
+ * Decode: exactly one query token per sequence (total_q == batch, and
+ * cu_seqlens_q = arange(batch + 1), which only the device reads: the rows of a
+ * sequence with another query count get out = 0 and lse = -inf).  Split-KV,
  * stream-K: pass 1 runs min(W, steps) persistent waves (W from the tile table:
  * 896 for 16-bit K/V, 2048 for fp8; ifa4_decode_tile reports it) over all
  * (sequence, kv head) caches laid end to end in 32-key steps, each wave an

@@ -160,13 +160,15 @@ __device__ __forceinline__ SeqChunk load_chunk(const DecodeParams& p, int base, 
   c.steps = 0;
   c.qs = c.ks = c.kbeg = c.kend = c.lk = 0;
   if (seq < p.batch) {
-    c.qs = p.cu_q[seq];
-    const int lq = p.cu_q[seq + 1] - c.qs;
+    const SeqBounds bq = seq_bounds(p.cu_q, seq, p.total_q);
+    c.qs = bq.start;
+    const int lq = bq.len;
     if constexpr (kPaged) {
       c.lk = paged_len(p, seq);
     } else {
-      c.ks = p.cu_k[seq];
-      c.lk = p.cu_k[seq + 1] - c.ks;
+      const SeqBounds bk = seq_bounds(p.cu_k, seq, p.total_k);
+      c.ks = bk.start;
+      c.lk = bk.len;
     }
     const KeyRange kr = decode_keys(p, c.lk);
     c.kbeg = kr.kbeg;
@@ -467,7 +469,7 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
       for (int h = 0; h < G; ++h) {
         const float a = readlane_f(alpha, h);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[h][e] *= a;
+        for (int e = 0; e < S::kEpl; ++e) o[h][e] *= a;
       }
     }
     wave_lds_sync();
@@ -600,12 +602,26 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
   const int ga = p.group;
   const int kvh = head / ga, h = head % ga;
   const int seg = seq * p.kv_heads + kvh;
-  const int qs = p.cu_q[seq];
-  const int lq = p.cu_q[seq + 1] - qs;
-  const int lk = p.block_table != nullptr ? paged_len(p, seq) : p.cu_k[seq + 1] - p.cu_k[seq];
+  const SeqBounds bq = seq_bounds(p.cu_q, seq, p.total_q);
+  const int qs = bq.start, lq = bq.len;
+  const int lk = p.block_table != nullptr ? paged_len(p, seq) : seq_bounds(p.cu_k, seq, p.total_k).len;
   const int meta_first = p.ws_meta[2 * seg];  // read before knowing it is needed
   const int meta_last = p.ws_meta[2 * seg + 1];
-  if (lq != 1) return;
+  if (lq != 1) {
+    // Not one query token (cu_seqlens_q is not arange): the pass above streamed
+    // nothing for this sequence; its query rows, if any, get out = 0, lse = -inf.
+    for (int row = wave; row < lq; row += kCombineWaves) {
+      uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)(qs + row) * p.o_st +
+                      (int64_t)head * p.o_sh + kPer * lane;
+      if constexpr (kPer == 2) {
+        *reinterpret_cast<uint32_t*>(dst) = 0u;
+      } else {
+        *dst = 0;
+      }
+      if (p.lse != nullptr && lane == 0) p.lse[(int64_t)head * p.lse_sh + qs + row] = -INFINITY;
+    }
+    return;
+  }
   int w_first = 0, parts = 0;
   if (seq_steps(lq, decode_keys(p, lk)) > 0 && p.n_waves > 0) {
     // clamped so that a slot index can never leave the workspace

@@ -21,6 +21,10 @@ constexpr float kLog2eHost = 1.4426950408889634f;
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Row counts as the kernels take them (cu_seqlens are clamped to these on the
+// device); a row index past INT32_MAX is not addressable there anyway.
+int32_t clamp_rows(int64_t n) { return n < INT32_MAX ? (int32_t)n : INT32_MAX; }
+
 // kv != nullptr: K/V are a paged cache described by *kv (checked by
 // check_paged); cu_seqlens_k is then not read and may be NULL.
 // kv_esize: bytes per K/V element (2, or 1 for an fp8 cache).
@@ -135,6 +139,8 @@ ifa4::PrefillParams make_prefill_params(const ifa4_args* a) {
   p.o_st = a->out_stride_t;
   p.o_sh = a->out_stride_h;
   p.lse_sh = a->lse_stride_h;
+  p.total_q = clamp_rows(a->total_q);
+  p.total_k = clamp_rows(a->total_k);
   p.batch = a->batch;
   p.n_heads = a->n_heads;
   p.group = a->n_heads / a->kv_heads;
@@ -235,6 +241,8 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
   p.o_st = args->out_stride_t;
   p.o_sh = args->out_stride_h;
   p.lse_sh = args->lse_stride_h;
+  p.total_q = clamp_rows(args->total_q);
+  p.total_k = clamp_rows(args->total_k);
   p.batch = args->batch;
   p.n_heads = args->n_heads;
   p.kv_heads = args->kv_heads;

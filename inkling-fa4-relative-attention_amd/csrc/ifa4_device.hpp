@@ -133,6 +133,18 @@ __device__ __forceinline__ float max_xor16(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Rows [start, start + len) of sequence `seq` from a cu_seqlens array, clamped
+// to [0, total]: offsets that are out of range or decreasing give a shorter (or
+// empty) sequence instead of reads and writes outside the tensors.
+struct SeqBounds {
+  int start, len;
+};
+__device__ __forceinline__ SeqBounds seq_bounds(const int32_t* cu, int seq, int total) {
+  const int s = min(max(cu[seq], 0), total);
+  const int e = min(max(cu[seq + 1], s), total);
+  return SeqBounds{s, e - s};
+}
+
 // Value of x in lane `src` (wave-uniform index), broadcast.
 __device__ __forceinline__ float readlane_f(float x, int src) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), src));

@@ -17,6 +17,8 @@ struct PrefillParams {
   const int32_t* cu_q;
   const int32_t* cu_k;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, rel_st, rel_sh, o_st, o_sh, lse_sh;
+  int32_t total_q;      // rows of q / out (cu_seqlens_q is clamped to it)
+  int32_t total_k;      // rows of k / v (cu_seqlens_k is clamped to it)
   int32_t batch;
   int32_t n_heads;
   int32_t group;        // n_heads / kv_heads
@@ -49,6 +51,8 @@ struct DecodeParams {
   float* ws_lse;      // [batch * kv_heads + n_waves][group] (log2 domain)
   int32_t* ws_meta;   // [batch * kv_heads][2]: first and last wave of a segment
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh, rel_st, rel_sh, o_st, o_sh, lse_sh;
+  int32_t total_q;   // rows of q / out (cu_seqlens_q is clamped to it)
+  int32_t total_k;   // rows of k / v (cu_seqlens_k is clamped to it; unused when paged)
   int32_t batch;
   int32_t n_heads;
   int32_t kv_heads;

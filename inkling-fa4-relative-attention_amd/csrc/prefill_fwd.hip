@@ -130,10 +130,13 @@ constexpr int kLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
 
 // Bias table in LDS, for the layout where every token of the sequence shares
 // one per-head table (token stride 0): log2(e) * rel[dist] at index
-// kBiasPad + dist, zeros for dist outside [0, rel_extent).  A tile that has
-// bias sees dist in an interval of 32 + 64 - 1 values that meets
-// [0, rel_extent), so the padding covers every read: no range checks.
-constexpr int kBiasPad = 96;
+// kBiasPad + dist, zeros for dist outside [0, rel_extent).  A wave's tile that
+// has bias sees dist (over all 32 * kNqb lanes' rows, valid or not, and the
+// kBlockK keys) in an interval of 32 * kNqb + kBlockK - 1 values that meets
+// [0, rel_extent), so a padding of 32 * kNqb + kBlockK - 2 on both sides
+// covers every read: no range checks.
+constexpr int kBiasPad = (32 * kNqb + kBlockK - 2 + 31) / 32 * 32;
+static_assert(kBiasPad >= 32 * kNqb + kBlockK - 2, "bias table padding covers a tile's band");
 constexpr int kBiasLdsMax = 1024;  // longest table staged in LDS
 
 // Fused relative-logit projection (kProj): bias(i, dist) = sum_c r[i, c] *
@@ -198,10 +201,10 @@ void prefill_fwd_kernel(PrefillParams p) {
     seq = rem / p.n_heads;
   }
 
-  const int qs = p.cu_q[seq];
-  const int lq = p.cu_q[seq + 1] - qs;
-  const int ks = p.cu_k[seq];
-  const int lk = p.cu_k[seq + 1] - ks;
+  const SeqBounds bq = seq_bounds(p.cu_q, seq, p.total_q);
+  const SeqBounds bk = seq_bounds(p.cu_k, seq, p.total_k);
+  const int qs = bq.start, lq = bq.len;
+  const int ks = bk.start, lk = bk.len;
   const int q0 = qtile * kBlockQ;
   if (q0 >= lq) return;
   const int kvh = head / p.group;

@@ -27,7 +27,14 @@ Differences from the reference wrappers (all deliberate):
     (triton_kernel.py:105 passes only window_size[0]);
   * `arch` is accepted and ignored: gfx950 has one tile table;
   * a row with no visible key yields out = 0 and lse = -inf;
-  * every input is validated; errors raise instead of reading out of bounds.
+  * shapes, dtypes, strides and sizes are validated on the host and errors
+    raise; the contents of cu_seqlens stay on the device and are not checked
+    there against the contract (non-decreasing, from 0, ending within the
+    tensors), but each sequence's range is clamped to the tensors' rows, so a
+    malformed array yields unspecified results for its sequences, never an
+    access outside the tensors.  Decode additionally needs cu_seqlens_q =
+    arange(batch + 1): rows of a sequence with another query count get
+    out = 0 and lse = -inf.
 The decode entry point uses the same default scale as prefill (1/head_dim);
 the reference decode kernel uses 1/sqrt(head_dim)
 (triton_kernel_decode.py:57), inconsistent with its prefill kernel.
