@@ -259,6 +259,22 @@ int32_t ifa4_decode_quant_fwd(const ifa4_args* args, const ifa4_paged_kv* kv,
                               const ifa4_kv_quant* quant, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/*
+ * Allocation-free decode: ifa4_decode_fwd with the library's own workspace
+ * instead of a workspace argument.  No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The workspace is a
+ * device array of IFA4_DECODE_SCRATCH_BYTES that each GPU holds from the
+ * library's first use there until the process ends; a call that needs more
+ * (ifa4_decode_workspace_bytes) returns IFA4_EWORKSPACE before touching the
+ * device.  The call allocates and frees nothing.  Every call on one GPU shares
+ * that GPU's array, so calls that overlap in time on one GPU (other streams or
+ * host threads) race.  `stream` must belong to the current device (else
+ * IFA4_EINVAL).  Results are those of ifa4_decode_fwd on the same arguments.
+ */
+#define IFA4_DECODE_SCRATCH_BYTES (32u << 20)
+int32_t ifa4_decode_fwd_noalloc(const ifa4_args* args, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

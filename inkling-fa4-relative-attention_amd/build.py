@@ -22,7 +22,7 @@ BUILD = os.path.join(HERE, "_build")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
-LIB_SOURCES = ["prefill_fwd.hip", "decode_fwd.hip", "ifa4_api.cpp"]
+LIB_SOURCES = ["prefill_fwd.hip", "decode_fwd.hip", "decode_noalloc.hip", "ifa4_api.cpp"]
 LIB_NAME = "libifa4.so"
 EXT_NAME = "_ifa4_torch.so"
 

@@ -273,6 +273,20 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
 
 }  // namespace
 
+namespace ifa4 {
+
+int32_t decode_workspace_need(const ifa4_args* args, size_t* bytes) {
+  const int32_t st = check_decode(args);
+  *bytes = st == IFA4_OK && args->batch > 0 ? (size_t)decode_layout(args).total() : 0;
+  return st;
+}
+
+int32_t decode_run(const ifa4_args* args, void* workspace, size_t workspace_bytes, void* stream) {
+  return run_decode(args, nullptr, nullptr, workspace, workspace_bytes, stream);
+}
+
+}  // namespace ifa4
+
 extern "C" {
 
 const char* ifa4_status_str(int32_t status) {

@@ -3,7 +3,10 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
+
+struct ifa4_args;
 
 namespace ifa4 {
 
@@ -85,5 +88,11 @@ hipError_t launch_prefill(const PrefillParams& p, int head_dim, int qkv_dtype, h
 int decode_max_group();
 int decode_fp8_max_group();
 hipError_t launch_decode(const DecodeParams& p, int head_dim, int qkv_dtype, hipStream_t stream);
+
+// Common body of the contiguous 16-bit decode entry points (ifa4_api.cpp): the
+// host checks with the workspace bytes the call needs, and the call itself on
+// a caller-provided workspace.
+int32_t decode_workspace_need(const ifa4_args* args, size_t* bytes);
+int32_t decode_run(const ifa4_args* args, void* workspace, size_t workspace_bytes, void* stream);
 
 }  // namespace ifa4

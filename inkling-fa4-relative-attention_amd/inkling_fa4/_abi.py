@@ -97,6 +97,7 @@ SIGNATURES = {
     "ifa4_decode_workspace_bytes": (ctypes.c_size_t, [_P_ARGS]),
     "ifa4_decode_tile": (_c_int32, [_P_ARGS, _P_TILE]),
     "ifa4_decode_fwd": (_c_int32, [_P_ARGS, _vp, ctypes.c_size_t, _vp]),
+    "ifa4_decode_fwd_noalloc": (_c_int32, [_P_ARGS, _vp]),
     "ifa4_decode_paged_workspace_bytes": (ctypes.c_size_t, [_P_ARGS, _P_PAGED]),
     "ifa4_decode_paged_fwd": (_c_int32, [_P_ARGS, _P_PAGED, _vp, ctypes.c_size_t, _vp]),
     "ifa4_decode_quant_workspace_bytes": (ctypes.c_size_t, [_P_ARGS, _P_PAGED, _P_QUANT]),
