@@ -10,9 +10,13 @@ Also measured in the same run: split-KV decode (batch 64, one query per
 sequence, KV lengths U[1024,16384] seeded, non-causal so the whole cache is
 streamed) as KV GB/s against the 8 TB/s HBM peak, also with the same keys in
 a paged cache (blocks of 16 tokens, shuffled) and as an fp8 (e4m3) cache; the
-other prefill sequence
-lengths {1024, 2048, 8192}; and, as the CPU baseline, the fp32 CPU oracle over
-the whole headline batch (median of up to 3 passes, at most ~30 s).
+other prefill sequence lengths {1024, 2048, 8192}; the headline shape with a
+per-token bias (fp32 extent 128, bf16 extent 1024) and with the fused
+RelLogitsProj; the sliding-window chunked prefill (batch 16, window 63) with
+the KV tiles it visits; the reference's own benchmark config (batch 1,
+Hq = Hkv = 4, per-token bf16 bias of extent 1024, S 64..4096) next to its
+published latencies; and, as the CPU baseline, the fp32 CPU oracle over the
+whole headline batch (median of up to 3 passes, at most ~30 s).
 
 Usage:  python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-cpu]
         [--only prefill|decode|all] [--seq 4096]
@@ -147,6 +151,76 @@ def prefill_bias_variants(steps, warmup, seq_len=4096, batch=8):
         c.q, c.k, c.v, r, w, c.cu_q, c.cu_k, c.max_q, c.max_k, 128, causal=True,
         softmax_scale=c.scale), steps, warmup)
     return {"per_token_rel_ms": ms_tok, "rproj_ms": ms_proj}
+
+
+# The reference's published prefill latencies (RTX 3090, sm86, after tuning;
+# README.md:9-14) for its benchmark config (benchmarks/benchmark_prefill.py:20-49):
+# batch 1, Hq = Hkv = 4, head_dim 128, bf16, causal, per-token bf16 rel_logits of
+# extent 1024, 10 warmup + 50 timed calls of the wrapper between two events.
+REFERENCE_README_MS = {64: 0.103, 128: 0.102, 512: 0.104, 1024: 0.160, 2048: 0.359,
+                       4096: 1.037}
+
+
+def reference_config_bench(seq_lens=(64, 128, 256, 512, 1024, 2048, 4096)):
+    """The reference's own benchmark config at each of its sequence lengths,
+    timed like the reference times it (10 warmup calls, then 50 calls of the
+    operator between two events), after the usual clock settling."""
+    import torch
+    from inkling_fa4 import inkling_fa4_rel_attention, testing
+
+    rows = {}
+    for s in seq_lens:
+        case = testing.make_case("reference_config", [s], [s], 4, 4, 128, torch.bfloat16,
+                                 seed=7, rel_extent=1024, rel_table=False,
+                                 rel_dtype=torch.bfloat16, rel_std=1.0)
+        c = case.to("cuda")
+        args = c.args()
+        ms = time_gpu(lambda: inkling_fa4_rel_attention(*args, causal=True), 50, 10,
+                      settle_s=0.25)
+        flops_ref = 2.0 * s * s * 128 * 4  # benchmark_prefill.py:47
+        row = {"ms": round(ms, 5), "tflops_ref_formula": round(flops_ref / (ms * 1e-3) / 1e12, 3)}
+        if s in REFERENCE_README_MS:
+            row["reference_rtx3090_ms"] = REFERENCE_README_MS[s]
+        rows[str(s)] = row
+        log(f"reference config seq {s}: {ms:.4f} ms")
+    return {"batch": 1, "n_heads": 4, "kv_heads": 4, "head_dim": 128, "rel_extent": 1024,
+            "rel": "per-token bf16", "causal": True, "seq": rows}
+
+
+def window_chunked_bench(steps, warmup):
+    """Sliding-window chunked prefill: batch 16, 128 new tokens over a 384-key
+    cache, window 63, causal; FLOPs of the visible pairs and the KV tiles the
+    kernel visits against an unpruned kernel."""
+    from inkling_fa4 import inkling_fa4_rel_attention, prefill_tile_counts, testing
+
+    case = testing.window_chunked()
+    flops = 4.0 * case.q.shape[2] * case.visible_pairs()
+    visited, total = prefill_tile_counts(case.cu_q, case.cu_k, case.q.shape[1], causal=True,
+                                         window_size=case.window_size)
+    c = case.to("cuda")
+    args = c.args()
+    ms = time_gpu(lambda: inkling_fa4_rel_attention(*args, causal=True,
+                                                    window_size=c.window_size), steps, warmup)
+    return {"ms": round(ms, 5), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+            "flops": flops, "kv_tiles_visited": visited, "kv_tiles_total": total}
+
+
+def per_token_bias_bench(steps, warmup, rel_extent, seq_len=4096, batch=8):
+    """The headline shape with a per-token bf16 rel_logits [Tq, Hq, rel_extent]
+    (the reference's benchmark and test layout)."""
+    import torch
+    from inkling_fa4 import inkling_fa4_rel_attention, testing
+
+    case = testing.make_case("per_token_bf16", [seq_len] * batch, [seq_len] * batch, 8, 2, 128,
+                             torch.bfloat16, seed=8, rel_extent=rel_extent, rel_table=False,
+                             rel_dtype=torch.bfloat16)
+    flops = 4.0 * 128 * case.visible_pairs()
+    c = case.to("cuda")
+    args = c.args()
+    ms = time_gpu(lambda: inkling_fa4_rel_attention(*args, causal=True), steps, warmup)
+    return {"rel_extent": rel_extent, "ms": round(ms, 5),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "rel_bytes": case.rel.numel() * case.rel.element_size()}
 
 
 def decode_bench(steps, warmup, block_size=0, fp8=False):
@@ -387,6 +461,16 @@ def main():
             log(f"prefill seq {args.seq}, per-token bias: {bv['per_token_rel_ms']:.4f} ms; "
                 f"fused RelLogitsProj: {bv['rproj_ms']:.4f} ms")
             result["prefill_bias_variants"] = {k: round(v, 5) for k, v in bv.items()}
+            pt = per_token_bias_bench(max(5, args.steps // 2), max(2, args.warmup // 2), 1024,
+                                      args.seq)
+            log(f"prefill seq {args.seq}, per-token bf16 bias, rel_extent 1024: "
+                f"{pt['ms']:.4f} ms  {pt['tflops']:.1f} TFLOP/s")
+            result["prefill_bias_variants"]["per_token_bf16_rel1024"] = pt
+            wc = window_chunked_bench(args.steps, args.warmup)
+            log(f"window + chunked prefill (batch 16, 128 over 384 keys, window 63): "
+                f"{wc['ms']:.4f} ms, KV tiles {wc['kv_tiles_visited']} of {wc['kv_tiles_total']}")
+            result["window_chunked"] = wc
+            result["reference_config"] = reference_config_bench()
     if args.only in ("all", "decode"):
         log(f"decode: {args.steps} steps")
         dec = decode_bench(args.steps, args.warmup)
