@@ -59,6 +59,9 @@ typedef enum ifa4_dtype {
  * The two agree when Lq == Lk.
  */
 #define IFA4_FLAG_BOTTOM_RIGHT 0x2u
+/* test: ifa4_prefill_fwd_ws splits every query tile's KV range into chunks of
+ * two KV tiles (exercises the split-KV merge on small inputs) */
+#define IFA4_FLAG_SPLIT_KV_2 0x4u
 
 /*
  * Arguments of one forward call.  Layouts (element strides, last dim contiguous):
@@ -160,6 +163,24 @@ int32_t ifa4_validate(const ifa4_args* args);
  * (NULL = the null stream).
  */
 int32_t ifa4_prefill_fwd(const ifa4_args* args, void* stream);
+
+/*
+ * Prefill with a workspace, for calls whose grid would leave the chip
+ * underfilled or unbalanced (few sequences or heads, short sequences): the
+ * tile table then cuts each query tile's KV range into chunks processed by
+ * separate workgroups (split KV), and a second pass merges the chunks' partial
+ * outputs by log-sum-exp.  ifa4_prefill_workspace_bytes gives the workspace
+ * the call needs, 0 when the table does not split it (ifa4_prefill_fwd_ws then
+ * runs exactly ifa4_prefill_fwd and the workspace may be NULL).  The workspace
+ * (256-byte aligned, contents on entry irrelevant) is scratch for one call;
+ * calls that share one must not overlap.  Results equal ifa4_prefill_fwd's up
+ * to the rounding of the merge.  Replaces the same launch loop as
+ * ifa4_prefill_fwd (src/inkling_fa4/triton_kernel.py:94-106), whose grid of
+ * (heads, query tiles) per sequence has the same underfill at small batch.
+ */
+size_t ifa4_prefill_workspace_bytes(const ifa4_args* args);
+int32_t ifa4_prefill_fwd_ws(const ifa4_args* args, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* Prefill with the fused relative-logit projection (ifa4_rel_proj). */
 int32_t ifa4_prefill_rproj_fwd(const ifa4_args* args, const ifa4_rel_proj* proj, void* stream);

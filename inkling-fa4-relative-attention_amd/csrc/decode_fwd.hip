@@ -46,6 +46,11 @@
 #ifndef IFA4_FP8_CVT2
 #define IFA4_FP8_CVT2 1
 #endif
+// Register budget of the stream pass: at least this many waves per SIMD
+// (2: at most 256 VGPRs, so that 2048 persistent waves fit in one round).
+#ifndef IFA4_DECODE_WPE
+#define IFA4_DECODE_WPE 2
+#endif
 
 namespace ifa4 {
 namespace {
@@ -62,7 +67,7 @@ __device__ __forceinline__ u32x4_t kv_load(rsrc_t r, uint32_t byte_off) {
   return buf_load_16(r, byte_off);
 #endif
 }
-constexpr int kDecodeFp8MaxGroup = 8;
+constexpr int kDecodeFp8MaxGroup = 16;
 
 // Lane layouts of a decode wave (D = head_dim, Eb = bytes per K/V element):
 //   row layout (loads, PV):  r = lane / kLpr is the row within a wave load,
@@ -77,7 +82,20 @@ struct DecodeShape {
   static constexpr int kGroupRows = kRpi > 8 ? kRpi : 8;  // paged: rows per resource
   static constexpr int kPitch = D + 8;         // LDS K row pitch (elements)
   static constexpr int kKSteps = D / 32;       // 16x16x32 MFMAs per 16 keys
+  static constexpr int kChunks = D / 8;        // 16-byte chunks of a 16-bit row
+  static constexpr int kDBlocks = D / 16;      // 16-row blocks of O^T (PV MFMAs per step)
 };
+
+// V tile of one step in LDS: [kStep][D] 16-bit, row-major, unpadded; chunk c of
+// row r sits at chunk c ^ vswz(r).  A transposing read of the PV A operand
+// covers four consecutive rows and one chunk pair per 16-lane group, eight
+// consecutive rows per half wave: the swizzle gives those rows distinct chunk
+// pairs (and, with two rows per 256-byte bank line at D = 64, distinct halves).
+template <int D>
+__device__ __forceinline__ int vswz(int row) {
+  constexpr int kRowsPerLine = 128 / D;
+  return 2 * ((row / kRowsPerLine) & (D / 16 - 1));
+}
 
 // 8 fp8 (OCP e4m3) values in two dwords (byte i = element i) -> fp32, exactly;
 // every e4m3 value is also exact in bf16 and fp16.
@@ -197,14 +215,14 @@ __device__ __forceinline__ int step_key0(const Cursor& cu) {
 }
 
 template <int D, typename Tag, int G, bool kPaged, int Eb>
-__global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_WPE, 8))) void decode_stream_kernel(DecodeParams p) {
   using E = Elem<Tag>;
   using S = DecodeShape<D, Eb>;
 
   __shared__ __align__(16) uint16_t k_lds[kStep * S::kPitch];
+  __shared__ __align__(16) uint16_t v_lds[kStep * D];
   using Q = DecodeQ<D, G>;
   __shared__ __align__(1024) uint16_t q_lds[2][Q::kElems];
-  __shared__ float p_lds[kStep * G];
 
   const int w = blockIdx.x;
   const int W = p.n_waves;
@@ -349,7 +367,9 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
   const float c2 = p.scale_log2;
   float m_run = -INFINITY;  // per head n (S^T lanes), identical over g
   float l_run = 0.f;        // partial sum over this lane's keys
-  float o[G][S::kEpl];
+  // O^T = V^T P^T in the 16x16 C layout: lane (n, g) holds d = 16 db + 4 g + j
+  // of head n (columns n >= group are padding and never stored).
+  f32x4_t o[S::kDBlocks];
   u32x4_t qf[S::kKSteps];
 
   auto step = [&](const u32x4_t* kr, const u32x4_t* vr, const Cursor& cu, bool last) {
@@ -357,39 +377,45 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
       m_run = -INFINITY;
       l_run = 0.f;
 #pragma unroll
-      for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int e = 0; e < S::kEpl; ++e) o[h][e] = 0.f;
+      for (int db = 0; db < S::kDBlocks; ++db) o[db] = f32x4_t{};
       if (cu.step == 0 && lane == 0) {
         // this wave holds the segment's first step: record the covering waves
         p.ws_meta[2 * cu.seg] = w;
         p.ws_meta[2 * cu.seg + 1] = (cu.seg_g0 + cu.steps - 1) / P;
       }
     }
-    // K rows -> LDS (row-major, padded rows: conflict-free A-operand reads).
+    // K rows -> LDS (row-major, padded rows: conflict-free A-operand reads of
+    // QK), V rows -> LDS (swizzled: conflict-free transposing reads of PV).
+    // fp8 converts to the MFMA type on the way (exact); the K scale is folded
+    // into the logit scale, the V scale into the partial's normalisation.
     // Waiting for these loads also completes the (earlier) Q DMA of the segment.
 #pragma unroll
     for (int i = 0; i < S::kLoads; ++i) {
-      uint16_t* dst = k_lds + (S::kRpi * i + r) * S::kPitch + S::kEpl * c;
+      const int row = S::kRpi * i + r;
+      uint16_t* kdst = k_lds + row * S::kPitch + S::kEpl * c;
       if constexpr (Eb == 2) {
-        *reinterpret_cast<u32x4_t*>(dst) = kr[i];
+        *reinterpret_cast<u32x4_t*>(kdst) = kr[i];
+        *reinterpret_cast<u32x4_t*>(v_lds + row * D + 8 * (c ^ vswz<D>(row))) = vr[i];
       } else {
-        // fp8 -> the MFMA type (exact); the K scale is folded into the logit scale
 #pragma unroll
         for (int hlf = 0; hlf < 2; ++hlf) {
 #if IFA4_FP8_CVT2
           // one conversion per pair, straight to the 16-bit type
           const uint32_t w0 = kr[i][2 * hlf], w1 = kr[i][2 * hlf + 1];
-          *reinterpret_cast<u32x4_t*>(dst + 8 * hlf) =
+          *reinterpret_cast<u32x4_t*>(kdst + 8 * hlf) =
               u32x4_t{E::template fp8x2<false>(w0), E::template fp8x2<true>(w0),
                       E::template fp8x2<false>(w1), E::template fp8x2<true>(w1)};
 #else
           float f[8];
           fp8x8_to_f32(kr[i][2 * hlf], kr[i][2 * hlf + 1], f);
-          *reinterpret_cast<u32x4_t*>(dst + 8 * hlf) =
+          *reinterpret_cast<u32x4_t*>(kdst + 8 * hlf) =
               u32x4_t{E::pack2(f[0], f[1]), E::pack2(f[2], f[3]), E::pack2(f[4], f[5]),
                       E::pack2(f[6], f[7])};
 #endif
+          const uint32_t x0 = vr[i][2 * hlf], x1 = vr[i][2 * hlf + 1];
+          *reinterpret_cast<u32x4_t*>(v_lds + row * D + 8 * ((2 * c + hlf) ^ vswz<D>(row))) =
+              u32x4_t{E::template fp8x2<false>(x0), E::template fp8x2<true>(x0),
+                      E::template fp8x2<false>(x1), E::template fp8x2<true>(x1)};
         }
       }
     }
@@ -454,81 +480,54 @@ __global__ __launch_bounds__(64) void decode_stream_kernel(DecodeParams p) {
       m_run = m_upd;
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    // P^T as the B operand of O^T += V^T P^T: column n = head, k-slots 0..3 =
+    // keys 4g..4g+3, 4..7 = keys 16+4g..16+4g+3 (where the S^T layout left them)
+    float pv[kStep / 16][4];
 #pragma unroll
     for (int blk = 0; blk < kStep / 16; ++blk) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float pv = fast_exp2(acc[blk][j] - m_use);
-        l_run += pv;
-        if (n < G) p_lds[(16 * blk + 4 * g + j) * G + n] = pv;
+        pv[blk][j] = fast_exp2(acc[blk][j] - m_use);
+        l_run += pv[blk][j];
       }
     }
+    const u32x4_t pb = {E::pack2(pv[0][0], pv[0][1]), E::pack2(pv[0][2], pv[0][3]),
+                        E::pack2(pv[1][0], pv[1][1]), E::pack2(pv[1][2], pv[1][3])};
     if (any_grow) {
-      // head h's factor sits in lane h (S^T layout, g = 0)
+      // lane (n, g) holds rows of head n, whose factor it computed itself
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float a = readlane_f(alpha, h);
-#pragma unroll
-        for (int e = 0; e < S::kEpl; ++e) o[h][e] *= a;
-      }
+      for (int db = 0; db < S::kDBlocks; ++db) o[db] *= alpha;
     }
-    wave_lds_sync();
 
-    // O += P V (VALU): row layout, key S::kRpi*i + r of the step
+    // O^T += V^T P^T on v_mfma_f32_16x16x32: A = V^T (row d, the same key
+    // k-slots as P), two transposing reads: 16-lane group g, lane i points at
+    // V[k0 + i/4][16 db + 4 (i % 4)] and receives V[k0 .. k0+3][16 db + i].
 #pragma unroll
-    for (int i = 0; i < S::kLoads; ++i) {
-      const int kl = S::kRpi * i + r;
-      float vv[S::kEpl];
-      if constexpr (Eb == 2) {
+    for (int db = 0; db < S::kDBlocks; ++db) {
+      u32x2_t part[2];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          vv[2 * q] = E::lo(vr[i][q]);
-          vv[2 * q + 1] = E::hi(vr[i][q]);
-        }
-      } else {
-        fp8x8_to_f32(vr[i][0], vr[i][1], vv);
-        fp8x8_to_f32(vr[i][2], vr[i][3], vv + 8);
+      for (int blk = 0; blk < 2; ++blk) {
+        const int row = 16 * blk + 4 * g + (n >> 2);
+        const int chunk = 2 * db + ((n & 3) >> 1);
+        const uint16_t* src = v_lds + row * D + 8 * (chunk ^ vswz<D>(row)) + 4 * (n & 1);
+        part[blk] = __builtin_bit_cast(
+            u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                         (__attribute__((address_space(3))) s16x4_t*)src));
       }
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float ph = p_lds[kl * G + h];
-#pragma unroll
-        for (int e = 0; e < S::kEpl; ++e) o[h][e] = fmaf(ph, vv[e], o[h][e]);
-      }
+      o[db] = E::mfma16(u32x4_t{part[0][0], part[0][1], part[1][0], part[1][1]}, pb, o[db]);
     }
-    wave_lds_sync();  // p_lds is rewritten by the next step
+    wave_lds_sync();  // k_lds / v_lds are rewritten by the next step
 
     if (!last) return;
-    // ---- partial of (segment, wave): reduce over lanes, normalise, store ---------
+    // ---- partial of (segment, wave): normalise, store ------------------------------
     const float l_tot = add_xor32(add_xor16(l_run));  // per head n, all g
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int e = 0; e < S::kEpl; ++e) {
-        float v = o[h][e];
-#pragma unroll
-        for (int off = S::kLpr; off < 64; off <<= 1) {
-          if (off < 16) v += __shfl_xor(v, off);
-          else if (off == 16) v = add_xor16(v);
-          else v = add_xor32(v);
-        }
-        o[h][e] = v;
-      }
     const int slot = cu.seg + w;
-    if (r == 0) {
+    if (n < g_act) {
+      const float inv = l_tot > 0.f ? p.v_scale / l_tot : 0.f;  // V scale (1 for 16-bit V)
+      float* dst = p.ws_o + ((int64_t)slot * g_act + n) * D + 4 * g;
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        if (h < g_act) {
-          const float lt = readlane_f(l_tot, h);
-          const float inv = lt > 0.f ? p.v_scale / lt : 0.f;  // V scale (1 for 16-bit V)
-          float* dst = p.ws_o + ((int64_t)slot * g_act + h) * D + S::kEpl * c;
-#pragma unroll
-          for (int q = 0; q < S::kEpl / 4; ++q)
-            *reinterpret_cast<f32x4_t*>(dst + 4 * q) =
-                f32x4_t{o[h][4 * q] * inv, o[h][4 * q + 1] * inv, o[h][4 * q + 2] * inv,
-                        o[h][4 * q + 3] * inv};
-        }
-      }
+      for (int db = 0; db < S::kDBlocks; ++db)
+        *reinterpret_cast<f32x4_t*>(dst + 16 * db) = o[db] * inv;
     }
     if (g == 0 && n < g_act) {
       const float lse2 = l_tot > 0.f ? m_run + __log2f(l_tot) : -INFINITY;
@@ -694,17 +693,10 @@ hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   if (p.n_waves > 0) {
     const dim3 grid(p.n_waves), block(64);
     if (p.kv_fp8) {
-      // fp8 K/V: 16 elements per lane, so o[G][16]; up to G = 8 fits in registers
-      if constexpr (G <= kDecodeFp8MaxGroup) {
-        if (p.block_table != nullptr)
-          hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 1>), grid, block, 0, stream,
-                             p);
-        else
-          hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 1>), grid, block, 0, stream,
-                             p);
-      } else {
-        return hipErrorInvalidValue;  // rejected on the host before any launch
-      }
+      if (p.block_table != nullptr)
+        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 1>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 1>), grid, block, 0, stream, p);
     } else {
       if (p.block_table != nullptr)
         hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 2>), grid, block, 0, stream, p);

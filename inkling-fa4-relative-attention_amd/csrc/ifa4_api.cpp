@@ -154,7 +154,32 @@ ifa4::PrefillParams make_prefill_params(const ifa4_args* a) {
   const int bq = ifa4::prefill_block_q();
   p.n_qtiles = (a->max_seqlen_q + bq - 1) / bq;
   p.scale_log2 = a->softmax_scale * kLog2eHost;
+  p.chunk_tiles = 0;
+  p.n_chunks = 1;
   return p;
+}
+
+// Split-KV plan of a prefill call and the workspace it needs: partial O
+// [n_chunks][n_heads][total_q][head_dim] fp32, then their LSEs, 256-byte aligned.
+struct PrefillWorkspace {
+  ifa4::PrefillSplit split;
+  int64_t o_bytes, lse_bytes;
+  int64_t total() const { return split.chunk_tiles > 0 ? o_bytes + lse_bytes : 0; }
+};
+PrefillWorkspace prefill_workspace(const ifa4_args* a) {
+  PrefillWorkspace w;
+  const bool bottom_right = (a->flags & IFA4_FLAG_BOTTOM_RIGHT) != 0;
+  // bottom-right masks see the last max_seqlen_q keys' positions: estimate with
+  // the full key range visible (causal off), which only shifts the heuristic
+  w.split = ifa4::prefill_split_for(a->batch, a->n_heads, a->max_seqlen_q, a->max_seqlen_k,
+                                    a->causal != 0 && !bottom_right,
+                                    bottom_right ? -1 : a->window_left, ifa4::prefill_block_q(),
+                                    ifa4::prefill_block_k(),
+                                    (a->flags & IFA4_FLAG_SPLIT_KV_2) ? 2 : 0);
+  const int64_t rows = (int64_t)w.split.n_chunks * a->n_heads * a->total_q;
+  w.o_bytes = (rows * a->head_dim * 4 + 255) / 256 * 256;
+  w.lse_bytes = (rows * 4 + 255) / 256 * 256;
+  return w;
 }
 
 // Top-left causal decode (Lq = 1) sees key 0 only.
@@ -324,6 +349,31 @@ int32_t ifa4_prefill_fwd(const ifa4_args* args, void* stream) {
   if (st != IFA4_OK) return st;
   if (args->batch == 0 || args->max_seqlen_q == 0) return IFA4_OK;
   const ifa4::PrefillParams p = make_prefill_params(args);
+  const hipError_t e = ifa4::launch_prefill(p, args->head_dim, args->qkv_dtype,
+                                            static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? IFA4_OK : IFA4_ELAUNCH;
+}
+
+size_t ifa4_prefill_workspace_bytes(const ifa4_args* args) {
+  if (check_args(args) != IFA4_OK || args->batch == 0 || args->max_seqlen_q == 0) return 0;
+  return (size_t)prefill_workspace(args).total();
+}
+
+int32_t ifa4_prefill_fwd_ws(const ifa4_args* args, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  const int32_t st = check_args(args);
+  if (st != IFA4_OK) return st;
+  if (args->batch == 0 || args->max_seqlen_q == 0) return IFA4_OK;
+  ifa4::PrefillParams p = make_prefill_params(args);
+  const PrefillWorkspace w = prefill_workspace(args);
+  if (w.total() > 0) {
+    if (workspace == nullptr || workspace_bytes < (size_t)w.total() || !aligned(workspace, 256))
+      return IFA4_EWORKSPACE;
+    p.chunk_tiles = w.split.chunk_tiles;
+    p.n_chunks = w.split.n_chunks;
+    p.part_o = static_cast<float*>(workspace);
+    p.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.o_bytes);
+  }
   const hipError_t e = ifa4::launch_prefill(p, args->head_dim, args->qkv_dtype,
                                             static_cast<hipStream_t>(stream));
   return e == hipSuccess ? IFA4_OK : IFA4_ELAUNCH;

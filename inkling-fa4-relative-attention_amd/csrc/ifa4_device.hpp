@@ -161,6 +161,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 __device__ __forceinline__ bool wave_any(bool p) {
   return __builtin_amdgcn_ballot_w64(p) != 0;
 }
+__device__ __forceinline__ bool wave_all(bool p) { return !wave_any(!p); }
 
 __device__ __forceinline__ u32x4_t ld_global_16(const void* p) {
   return *reinterpret_cast<const u32x4_t*>(p);
@@ -255,11 +256,20 @@ struct RelBf16 {
   static __device__ __forceinline__ float load(rsrc_t r, uint32_t off) {
     return __uint_as_float(buf_load_2(r, off) << 16);
   }
+  // element 0 / 1 of a packed pair
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 };
 struct RelF16 {
   static constexpr int kBytes = 2;
   static __device__ __forceinline__ float load(rsrc_t r, uint32_t off) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)buf_load_2(r, off));
+  }
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
   }
 };
 

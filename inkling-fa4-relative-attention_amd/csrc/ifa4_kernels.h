@@ -35,6 +35,15 @@ struct PrefillParams {
   int32_t n_qtiles;     // ceil(max_seqlen_q / block_q)
   int32_t xcd_pairs;    // (sequence, kv head) pairs per XCD in the XCD-aware order, or 0
   float scale_log2;     // softmax_scale * log2(e)
+  // Split KV (chunk_tiles > 0): each q tile's KV tile range is cut into chunks
+  // of chunk_tiles tiles, one workgroup each (n_chunks chunk slots per q tile in
+  // the grid); a tile with more than one chunk writes normalised partials
+  // part_o [n_chunks][n_heads][total_q][head_dim] fp32 and their LSE (log2
+  // units) part_lse [n_chunks][n_heads][total_q], merged by a second pass.
+  int32_t chunk_tiles;
+  int32_t n_chunks;
+  float* part_o;
+  float* part_lse;
   // Fused relative-logit projection (wt != nullptr): rel / rel_st / rel_sh /
   // rel_dtype describe r [Tq, Hq, 16]; wt is W^T [rel_width, 16] fp32, rows
   // contiguous; bias(i, dist) = sum_c r[i, c] * wt[dist, c].

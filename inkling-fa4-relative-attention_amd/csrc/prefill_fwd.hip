@@ -82,18 +82,35 @@
 namespace ifa4 {
 namespace {
 
-constexpr int kNqb = IFA4_PREFILL_NQB;           // 32-row query blocks per wave
-constexpr int kWaves = kNqb == 1 ? 4 : 2;        // waves per workgroup
-constexpr int kBlockQ = 32 * kNqb * kWaves;      // 128
+// Tile shape of one instantiation of the kernel.
+template <int NQB, int BK, int WPE>
+struct PrefillShape {
+  static constexpr int kNqb = NQB;                    // 32-row query blocks per wave
+  static constexpr int kWaves = NQB == 1 ? 4 : 2;     // waves per workgroup
+  static constexpr int kBlockQ = 32 * NQB * kWaves;   // 128
+  static constexpr int kBlockK = BK;                  // keys per KV tile (32 or 64)
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kWavesPerSimd = WPE;           // occupancy the register budget targets
+  // Bias table in LDS, for the layout where every token of the sequence shares
+  // one per-head table (token stride 0): log2(e) * rel[dist] at index
+  // kBiasPad + dist, zeros for dist outside [0, rel_extent).  A wave's tile
+  // that has bias sees dist (over all 32 * NQB lanes' rows, valid or not, and
+  // the BK keys) in an interval of 32 * NQB + BK - 1 values that meets
+  // [0, rel_extent), so a padding of 32 * NQB + BK - 2 on both sides covers
+  // every read: no range checks.
+  static constexpr int kBiasPad = (32 * NQB + BK - 2 + 31) / 32 * 32;
+  static_assert(kBiasPad >= 32 * NQB + BK - 2, "bias table padding covers a tile's band");
+};
+
 #ifndef IFA4_BLOCK_K
 #define IFA4_BLOCK_K 64
 #endif
-constexpr int kBlockK = IFA4_BLOCK_K;            // keys per KV tile (32 or 64)
-constexpr int kThreads = 64 * kWaves;
 #ifndef IFA4_WPE
-#define IFA4_WPE (kNqb == 1 ? 2 : 1)
+#define IFA4_WPE (IFA4_PREFILL_NQB == 1 ? 2 : 1)
 #endif
-constexpr int kWavesPerSimd = IFA4_WPE;         // occupancy the register budget targets
+// The shape the library is built with (sweep knobs IFA4_PREFILL_NQB,
+// IFA4_BLOCK_K, IFA4_WPE).
+using Shape = PrefillShape<IFA4_PREFILL_NQB, IFA4_BLOCK_K, IFA4_WPE>;
 #ifndef IFA4_LOOK_K
 #define IFA4_LOOK_K 4
 #endif
@@ -104,23 +121,37 @@ constexpr int kWavesPerSimd = IFA4_WPE;         // occupancy the register budget
 [[maybe_unused]] constexpr int kLookV = IFA4_LOOK_V;  // V^T operand pairs in flight ahead of the PV MFMAs (PV2 off)
 
 // One LDS stage: K tile then V tile, each [kBlockK][D] row-major, swizzled.
-template <int D>
+template <typename Sh, int D>
 struct PrefillStage {
-  static constexpr int kTile = kBlockK * D;              // 16-bit elements per tensor
+  static constexpr int kTile = Sh::kBlockK * D;          // 16-bit elements per tensor
   static constexpr int kElems = 2 * kTile;
   static constexpr int kChunks = D / 8;                  // 16-byte chunks per row
   static constexpr int kRowsPerDma = 1024 / (2 * D);     // rows one wave DMA covers
-  static constexpr int kDmaPerTensor = kBlockK / kRowsPerDma;
-  static constexpr int kDmaPerWave = 2 * kDmaPerTensor / kWaves;
+  static constexpr int kDmaPerTensor = Sh::kBlockK / kRowsPerDma;
+  static constexpr int kDmaPerWave = 2 * kDmaPerTensor / Sh::kWaves;
 };
 
+// Keys of a 32-key block in the S^T tile: MFMA row r of S^T = K Q^T reads K
+// row perm32(r), so that lane half h, which holds rows 8i + 4h + j (i, j in
+// 0..3) of the 32x32 C layout, holds keys 16h + 4i + j: sixteen consecutive
+// keys, whose relative-bias distances are consecutive too.
+__device__ __forceinline__ int perm32(int r) {
+  return (((r >> 2) & 1) << 4) | ((r >> 3) << 2) | (r & 3);
+}
+
 // 16-byte chunk swizzle of an LDS row, kChunks = chunks per row (16 or 8).
-// Measured with the LDS bank-conflict counter on gfx950: zero conflicts for
-// both the 8-row K reads (ds_read_b128) and the 4-row transposing V reads
-// (ds_read_b64_tr_b16) at 16 chunks per row.
+// Chunk c of tile row `row` sits at chunk c ^ swz(row).  The QK A-operand reads
+// (ds_read_b128, 16 lanes per pass) cover rows {0..7, 16..23} or {8..15,
+// 24..31} of a 32-key block at one chunk; the transposing V reads of PV cover
+// four consecutive rows and four chunks per half wave: both are conflict-free
+// (every bank once per pass) for 16 chunks per row (d 128, one row per 256-byte
+// bank line) and 8 (d 64, two rows per line).
 template <int kChunks>
 __device__ __forceinline__ int swz(int row) {
-  return (((row & 3) << 2) | ((row >> 2) & 3)) & (kChunks - 1);
+  if constexpr (kChunks == 16)
+    return ((row & 3) << 2) | ((row >> 2) & 1) | (((row >> 4) & 1) << 1);
+  else
+    return (((row >> 1) & 1) << 2) | ((row >> 2) & 1) | (((row >> 4) & 1) << 1);
 }
 
 // s_waitcnt immediates: at most n vector-memory operations of this wave
@@ -128,16 +159,7 @@ __device__ __forceinline__ int swz(int row) {
 constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
 constexpr int kLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
 
-// Bias table in LDS, for the layout where every token of the sequence shares
-// one per-head table (token stride 0): log2(e) * rel[dist] at index
-// kBiasPad + dist, zeros for dist outside [0, rel_extent).  A wave's tile that
-// has bias sees dist (over all 32 * kNqb lanes' rows, valid or not, and the
-// kBlockK keys) in an interval of 32 * kNqb + kBlockK - 1 values that meets
-// [0, rel_extent), so a padding of 32 * kNqb + kBlockK - 2 on both sides
-// covers every read: no range checks.
-constexpr int kBiasPad = (32 * kNqb + kBlockK - 2 + 31) / 32 * 32;
-static_assert(kBiasPad >= 32 * kNqb + kBlockK - 2, "bias table padding covers a tile's band");
-constexpr int kBiasLdsMax = 1024;  // longest table staged in LDS
+constexpr int kBiasLdsMax = 1024;  // longest shared bias table staged in LDS
 
 // Fused relative-logit projection (kProj): bias(i, dist) = sum_c r[i, c] *
 // W[c, dist] with r [Tq, Hq, kProjDim] and W^T [R', kProjDim] fp32.  The
@@ -148,7 +170,6 @@ constexpr int kBiasLdsMax = 1024;  // longest table staged in LDS
 // once.  (A W^T read from L2 for longer extents needed ~100 more VGPRs.)
 constexpr int kProjDim = 16;
 constexpr int kWtLdsMax = 128;
-constexpr int kBiasLdsFloats = 2 * kBiasPad + kBiasLdsMax;           // 1216
 constexpr int kWtLdsFloats = kWtLdsMax * kProjDim;                   // 2048
 __device__ __forceinline__ int wt_lds_index(int d, int chunk) {
   return d * kProjDim + 4 * (chunk ^ ((d >> 2) & 3));
@@ -159,12 +180,47 @@ __device__ __forceinline__ uint32_t span_bytes(int rows, int64_t stride, int d, 
   return rows > 0 ? (uint32_t)(((int64_t)(rows - 1) * stride + d) * esize) : 0u;
 }
 
-template <int D, typename Tag, typename Rel, bool kProj>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kWavesPerSimd,
-                                                                          kWavesPerSimd)))
-void prefill_fwd_kernel(PrefillParams p) {
+// KV tiles [kt_beg, kt_end) a query tile visits (tile pruning): causal keeps
+// keys below the tile's last row (+ qpos), the window keys from its first row
+// (+ qpos) minus window_left; the prefill kernel and the merge of split-KV
+// partials both derive a tile's range (and so its chunk count) from this.
+struct TileRange {
+  int beg, end;
+};
+template <typename Sh>
+__device__ __forceinline__ TileRange tile_range(const PrefillParams& p, int q0, int lq, int lk,
+                                                int qpos) {
+  const int q_hi = min(q0 + Sh::kBlockQ, lq);  // exclusive
+  int kend = lk, kbeg = 0;
+  if (!p.no_prune) {
+    if (p.causal) kend = min(kend, q_hi + qpos);
+    if (p.window_left >= 0) kbeg = max(0, q0 + qpos - p.window_left);
+  }
+  const int beg = kbeg / Sh::kBlockK;
+  return TileRange{beg, kend > kbeg ? (kend + Sh::kBlockK - 1) / Sh::kBlockK : beg};
+}
+
+// Split KV: chunk c of the key axis holds KV tiles [c, c + 1) * chunk_tiles;
+// a query tile's k-th chunk is the k-th chunk its range meets, so the same
+// tiles fall in the same chunks whatever the pruning.  Chunks a query tile
+// spans: at least one (which also writes the rows of a tile with no visible
+// key), at most the n_chunks slots the grid and the workspace hold.
+__device__ __forceinline__ int tile_chunks(const PrefillParams& p, const TileRange& r) {
+  if (p.chunk_tiles <= 0) return 1;
+  const int n = r.end > r.beg ? (r.end + p.chunk_tiles - 1) / p.chunk_tiles -
+                                    r.beg / p.chunk_tiles
+                              : 1;
+  return min(max(n, 1), p.n_chunks);
+}
+
+template <typename Sh, int D, typename Tag, typename Rel, bool kProj>
+__global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
+    Sh::kWavesPerSimd, Sh::kWavesPerSimd))) void prefill_fwd_kernel(PrefillParams p) {
   using E = Elem<Tag>;
-  using St = PrefillStage<D>;
+  using St = PrefillStage<Sh, D>;
+  constexpr int kNqb = Sh::kNqb, kBlockQ = Sh::kBlockQ;
+  constexpr int kBlockK = Sh::kBlockK, kThreads = Sh::kThreads, kBiasPad = Sh::kBiasPad;
+  constexpr int kBiasLdsFloats = 2 * kBiasPad + kBiasLdsMax;
   constexpr int kDBlocks = D / 32;
   constexpr int kKSteps = D / 16;
 
@@ -178,15 +234,19 @@ void prefill_fwd_kernel(PrefillParams p) {
   uint16_t* const stage0 = stages;
   uint16_t* const stage1 = stages + St::kElems;
 
-  // ---- which (q tile, head, sequence): heaviest (last) q tiles first --------
-  int qtile, head, seq;
+  // ---- which (q tile, KV chunk, head, sequence): heaviest (last) q tiles first --
+  // A q tile's chunks (split KV; one when not splitting) are consecutive, so
+  // a chunk that ends early is followed by the next q tile's work.
+  int qtile, chunk, head, seq;
   if (p.xcd_pairs) {
     // Workgroup i runs on XCD i % 8.  Give XCD x the (sequence, kv head) pairs
     // x, x+8, ... so their K/V stay in that XCD's L2; heaviest q tiles first.
     const int x = blockIdx.x & 7, slot = blockIdx.x >> 3;
     const int per_xcd = p.xcd_pairs;  // pairs per XCD
     const int per_tile = per_xcd * p.group;
-    qtile = p.n_qtiles - 1 - slot / per_tile;
+    const int qc = slot / per_tile;
+    qtile = p.n_qtiles - 1 - qc / p.n_chunks;
+    chunk = qc % p.n_chunks;
     const int rem = slot % per_tile;
     const int pair = x + 8 * (rem / p.group);
     const int kv_heads = p.n_heads / p.group;
@@ -195,7 +255,9 @@ void prefill_fwd_kernel(PrefillParams p) {
   } else {
     const int per_tile = p.n_heads * p.batch;
     const int lin = blockIdx.x;
-    qtile = p.n_qtiles - 1 - lin / per_tile;
+    const int qc = lin / per_tile;
+    qtile = p.n_qtiles - 1 - qc / p.n_chunks;
+    chunk = qc % p.n_chunks;
     const int rem = lin % per_tile;
     head = rem % p.n_heads;
     seq = rem / p.n_heads;
@@ -235,15 +297,16 @@ void prefill_fwd_kernel(PrefillParams p) {
   const rsrc_t rv = make_rsrc(v_base, span_bytes(lk, p.v_st, D, 2));
   const uint32_t k_row = (uint32_t)p.k_st * 2, v_row = (uint32_t)p.v_st * 2;
 
-  // ---- key range of the workgroup (tile pruning) ---------------------------
-  const int q_hi = min(q0 + kBlockQ, lq);  // exclusive
-  int kend = lk, kbeg = 0;
-  if (!p.no_prune) {
-    if (p.causal) kend = min(kend, q_hi + qpos);
-    if (wl >= 0) kbeg = max(0, q0 + qpos - wl);
+  // ---- key range of the workgroup (tile pruning, then this KV chunk) ---------
+  const TileRange tr = tile_range<Sh>(p, q0, lq, lk, qpos);
+  const int nch = tile_chunks(p, tr);
+  if (chunk >= nch) return;
+  int kt_beg = tr.beg, kt_end = tr.end;
+  if (nch > 1) {
+    const int c0 = (tr.beg / p.chunk_tiles + chunk) * p.chunk_tiles;
+    kt_beg = max(tr.beg, c0);
+    kt_end = min(tr.end, c0 + p.chunk_tiles);
   }
-  const int kt_beg = kbeg / kBlockK;
-  const int kt_end = kend > kbeg ? (kend + kBlockK - 1) / kBlockK : kt_beg;
 
   // ---- per-wave rows ---------------------------------------------------------
   const int qa = q0 + 32 * kNqb * wave;                  // first row of the wave (local)
@@ -291,9 +354,11 @@ void prefill_fwd_kernel(PrefillParams p) {
   // the second).  A lane's offset within a DMA depends on the tile only through
   // kb (added as the scalar offset) and on the block only through the swizzle
   // phase (blk % kPhases) and a row shift (also scalar): kPhases registers, set once.
-  constexpr int kPhases = 16 / St::kRowsPerDma;
+  constexpr int kPhases = 32 / St::kRowsPerDma;  // the swizzle repeats every 32 rows
   static_assert(St::kDmaPerWave <= St::kDmaPerTensor && St::kDmaPerTensor % St::kDmaPerWave == 0,
                 "a wave's DMAs stay within one tensor");
+  static_assert(St::kDmaPerWave % kPhases == 0 && St::kDmaPerTensor % kPhases == 0,
+                "a DMA's swizzle phase is its index within the wave's batch");
   const bool dma_v = wave * St::kDmaPerWave >= St::kDmaPerTensor;
   const uint32_t dma_rowb = dma_v ? v_row : k_row;
   const rsrc_t dma_r = dma_v ? rv : rk;
@@ -362,7 +427,7 @@ void prefill_fwd_kernel(PrefillParams p) {
           const f32x4_t r4 = *reinterpret_cast<const f32x4_t*>(r_lds + wt_lds_index(row, ch));
 #pragma unroll
           for (int e = 4 * eg; e < 4 * eg + 4; ++e) {
-            const int dist = dbase - (32 * blk + 8 * (e >> 2) + (e & 3));
+            const int dist = dbase - (32 * blk + e);
             const int d = (uint32_t)dist < (uint32_t)rext ? dist : 0;
             const f32x4_t w = *reinterpret_cast<const f32x4_t*>(bias_lds + wt_lds_index(d, ch));
 #pragma unroll
@@ -374,16 +439,79 @@ void prefill_fwd_kernel(PrefillParams p) {
     }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int dist = dbase - (32 * blk + 8 * (e >> 2) + (e & 3));
+      const int dist = dbase - (32 * blk + e);
       bias[e] = (uint32_t)dist < (uint32_t)rext ? bias[e] * kLog2e : 0.f;
     }
   };
 
+  // Per-token bias of the 16 consecutive keys a lane holds in a 32-key block,
+  // at distances dtop - e (e = 0..15) of its row (element offset rel_row in the
+  // bias resource), times log2(e), zero outside [0, rel_extent).  The 16
+  // values are contiguous in memory: fp32 in four 16-byte loads, 16-bit types
+  // in nine dwords from the even element at or below the lowest (two 16-byte
+  // loads and one 4-byte load), shifted into place.  A wave with a valid row
+  // whose span would start before the resource (the first row of a sequence,
+  // or a token stride of 0) or end past it (the last row) falls back to one
+  // load per element, so no vector load straddles either end.
+  const int rel_par = Rel::kBytes == 2 ? (int)((reinterpret_cast<uintptr_t>(p.rel) +
+                                                ((int64_t)qs * p.rel_st + (int64_t)head * p.rel_sh) *
+                                                    Rel::kBytes) >> 1) & 1
+                                       : 0;  // element parity of the resource base
+  const int rel_span = lq > 0 ? (lq - 1) * (int)p.rel_st + p.rel_width : 0;  // elements
+  auto token_bias = [&](int rel_row, int dtop, bool valid, float* bias) {
+    constexpr int kSpan = Rel::kBytes == 2 ? 18 : 16;  // elements the vector loads cover
+    const int lo = rel_row + dtop - 15;               // element of the lowest distance
+    const int start = Rel::kBytes == 2 ? lo - ((lo + rel_par) & 1) : lo;  // dword-aligned
+    if (wave_any(valid && (start < 0 || start + kSpan > rel_span))) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int dist = dtop - e;
+        const uint32_t off = (uint32_t)dist < (uint32_t)rext
+                                 ? (uint32_t)(rel_row + dist) * Rel::kBytes
+                                 : kOutOfRange;
+        bias[e] = Rel::load(rrel, off) * kLog2e;
+      }
+      return;
+    }
+    const uint32_t boff = valid ? (uint32_t)start * Rel::kBytes : kOutOfRange;
+    if constexpr (Rel::kBytes == 4) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4_t w = buf_load_16(rrel, boff + 16 * c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bias[15 - (4 * c + j)] = __uint_as_float(w[j]);  // dist lo + 4c + j
+      }
+    } else {
+      const u32x4_t w0 = buf_load_16(rrel, boff);
+      const u32x4_t w1 = buf_load_16(rrel, boff + 16);
+      const uint32_t w2 = buf_load_4(rrel, boff + 32);
+      const uint32_t w[9] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3], w2};
+      const uint32_t sh = 16u * (uint32_t)(lo - start);  // 0 or 16 bits
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t pr = __builtin_amdgcn_alignbit(w[k + 1], w[k], sh);  // dist lo+2k, lo+2k+1
+        bias[15 - 2 * k] = Rel::lo(pr);
+        bias[14 - 2 * k] = Rel::hi(pr);
+      }
+    }
+    const bool in_band = dtop - 15 >= 0 && dtop < rext;
+    if (wave_all(in_band)) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) bias[e] *= kLog2e;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        bias[e] = (uint32_t)(dtop - e) < (uint32_t)rext ? bias[e] * kLog2e : 0.f;
+    }
+  };
+
   // Lane constants of the LDS fragment reads.
-  // K (A operand of QK): row 32*blk + col, chunk 2*kk + half.
+  // K (A operand of QK): row 32*blk + perm32(col), chunk 2*kk + half.
   // V^T (A operand of PV, two transposing reads): 16-lane group gq = lane / 16,
   // lane i = lane % 16 of the group addresses V[k0 + i/4][d0 + 4*(i%4)] with
-  // d0 = 32*db + 16*(gq % 2) and k0 = 16*t + 4*half (+ 8 for the second read).
+  // d0 = 32*db + 16*(gq % 2) and k0 = 32*(t/2) + 16*half + 8*(t%2) (+ 4 for the
+  // second read): the keys P holds for key block t (elements 8*(t%2) .. +7 of
+  // the S^T block t/2) in the same order.
   const int tr_i = lane & 15;
   const int tr_row = tr_i >> 2;                         // + k0
   const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (tr_i & 3);  // + 32*db
@@ -411,7 +539,7 @@ void prefill_fwd_kernel(PrefillParams p) {
     for (int blk = 0; blk < kBlockK / 32; ++blk) {
 #pragma unroll
       for (int qb = 0; qb < kNqb; ++qb) s[qb][blk] = f32x16_t{};
-      const int row = 32 * blk + col;
+      const int row = 32 * blk + perm32(col);
       const uint16_t* krow = kl + row * D;
       const int sw = swz<St::kChunks>(row);
 #pragma unroll
@@ -446,7 +574,7 @@ void prefill_fwd_kernel(PrefillParams p) {
       u32x2_t part[2];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const int row = 16 * t + 8 * r + 4 * half + tr_row;
+        const int row = 32 * (t >> 1) + 16 * half + 8 * (t & 1) + 4 * r + tr_row;
         const int c = 32 * db + tr_col;  // element column, multiple of 4
         const uint16_t* src = vl + row * D + 8 * ((c >> 3) ^ swz<St::kChunks>(row)) + (c & 7);
         part[r] = __builtin_bit_cast(
@@ -467,8 +595,8 @@ void prefill_fwd_kernel(PrefillParams p) {
 #endif
 
     // ---- logits (log2 domain) and tile max ---------------------------------------
-    // Element (blk, e) of a lane is tile-local key 32*blk + 8*(e>>2) + (e&3)
-    // + 4*half; `kc` below drops the lane term, which is folded into the bounds.
+    // Element (blk, e) of a lane is tile-local key 32*blk + 16*half + e; `kc`
+    // below drops the lane term, which is folded into the bounds.
     float sc;  // factor applied inside the exponent FMA
     float mx[kNqb];
     if (need_mask || has_bias) {
@@ -479,9 +607,9 @@ void prefill_fwd_kernel(PrefillParams p) {
         if (p.causal) hi = min(hi, qi[qb] + qpos - kb);
         if (!row_ok[qb]) hi = -1;
         const int lo = wl >= 0 ? qi[qb] + qpos - wl - kb : -1;
-        const int hi_h = hi - 4 * half, lo_h = lo - 4 * half;
-        const int dbase = qi[qb] + delta - kb - 4 * half;  // dist = dbase - kc
-        const uint32_t rel_row_off = (uint32_t)(qi[qb] * p.rel_st) * Rel::kBytes;
+        const int hi_h = hi - 16 * half, lo_h = lo - 16 * half;
+        const int dbase = qi[qb] + delta - kb - 16 * half;  // dist = dbase - kc
+        const int rel_row = qi[qb] * (int)p.rel_st;        // element offset of the row
         float m = -INFINITY;
 #pragma unroll
         for (int blk = 0; blk < kBlockK / 32; ++blk) {
@@ -490,26 +618,15 @@ void prefill_fwd_kernel(PrefillParams p) {
             // element e at dist = dbase - kc: a constant offset from one base
             const float* tb = bias_lds + kBiasPad + dbase - (kBlockK - 1);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
-              bias[e] = tb[kBlockK - 1 - kc];
-            }
+            for (int e = 0; e < 16; ++e) bias[e] = tb[kBlockK - 1 - (32 * blk + e)];
           } else if (has_bias && kProj) {
             proj_bias(dbase, blk, qi[qb] - q0, bias);
           } else if (has_bias) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-              const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
-              const int dist = dbase - kc;
-              const uint32_t off = (uint32_t)dist < (uint32_t)rext
-                                       ? rel_row_off + (uint32_t)dist * Rel::kBytes
-                                       : kOutOfRange;
-              bias[e] = Rel::load(rrel, off) * kLog2e;
-            }
+            token_bias(rel_row, dbase - 32 * blk, row_ok[qb], bias);
           }
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
-            const int kc = 32 * blk + 8 * (e >> 2) + (e & 3);
+            const int kc = 32 * blk + e;
             float x = s[qb][blk][e] * c2;
             if (has_bias) x += bias[e];
             if (need_mask) x = (kc >= lo_h && kc <= hi_h) ? x : -INFINITY;
@@ -655,7 +772,7 @@ void prefill_fwd_kernel(PrefillParams p) {
         u32x2_t part[2];
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-          const int row = 16 * t + 8 * r + 4 * half + tr_row;
+          const int row = 32 * (t >> 1) + 16 * half + 8 * (t & 1) + 4 * r + tr_row;
           const int c = 32 * db + tr_col;  // element column, multiple of 4
           const uint16_t* src = vl + row * D + 8 * ((c >> 3) ^ swz<St::kChunks>(row)) + (c & 7);
           part[r] = __builtin_bit_cast(
@@ -788,12 +905,24 @@ void prefill_fwd_kernel(PrefillParams p) {
     if (kt + 1 < kt_end) step(kt + 1, stage1, stage0);
   }
 
-  // ---- epilogue: normalise, store O and LSE ------------------------------------------
+  // ---- epilogue: normalise, store O and LSE (split KV: this chunk's partial) -----
 #pragma unroll
   for (int qb = 0; qb < kNqb; ++qb) {
     const float l_tot = add_xor32(l_run[qb]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (row_ok[qb]) {
+    if (row_ok[qb] && nch > 1) {
+      // normalised O of the chunk (fp32) and its LSE in log2 units
+      const int64_t prow = ((int64_t)chunk * p.n_heads + head) * p.total_q + qs + qi[qb];
+      float* pbase = p.part_o + prow * D;
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<f32x4_t*>(pbase + 32 * db + 8 * i + 4 * half) =
+              f32x4_t{o[qb][db][4 * i] * inv, o[qb][db][4 * i + 1] * inv,
+                      o[qb][db][4 * i + 2] * inv, o[qb][db][4 * i + 3] * inv};
+      if (half == 0) p.part_lse[prow] = l_tot > 0.f ? m_run[qb] + __log2f(l_tot) : -INFINITY;
+    } else if (row_ok[qb]) {
       uint16_t* obase = static_cast<uint16_t*>(p.out) + (int64_t)(qs + qi[qb]) * p.o_st +
                         (int64_t)head * p.o_sh;
 #pragma unroll
@@ -814,16 +943,106 @@ void prefill_fwd_kernel(PrefillParams p) {
   }
 }
 
+// Merge of split-KV partials (second pass after a split launch): kMergeParts
+// workgroups per (q tile, head, sequence), each a quarter of the tile's rows; a
+// tile whose range did not split was written by the prefill kernel itself and
+// is skipped.  32 threads share a row (head_dim / 32 consecutive d values each)
+// and a thread holds kRows rows; the chunks are the outer loop, so each thread
+// has kRows independent loads in flight per chunk while it merges online
+// (running max over the chunks' LSEs).
+constexpr int kMergeThreads = 256;
+constexpr int kMergeParts = 4;
+template <typename Sh, int D, typename Tag>
+__global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillParams p) {
+  using E = Elem<Tag>;
+  constexpr int kTpr = 32;                          // threads per row
+  constexpr int kPer = D / kTpr;                    // d values per thread
+  constexpr int kStride = kMergeThreads / kTpr;     // rows per pass of the workgroup
+  constexpr int kRows = Sh::kBlockQ / kMergeParts / kStride;  // rows per thread
+  const int qtile = blockIdx.x / kMergeParts, part = blockIdx.x % kMergeParts;
+  const int head = blockIdx.y, seq = blockIdx.z;
+  const SeqBounds bq = seq_bounds(p.cu_q, seq, p.total_q);
+  const SeqBounds bk = seq_bounds(p.cu_k, seq, p.total_k);
+  const int q0 = qtile * Sh::kBlockQ;
+  if (q0 >= bq.len) return;
+  const int qpos = p.bottom_right ? bk.len - bq.len : 0;
+  const int nch = tile_chunks(p, tile_range<Sh>(p, q0, bq.len, bk.len, qpos));
+  if (nch <= 1) return;
+  const int r0 = q0 + part * (Sh::kBlockQ / kMergeParts) + (int)threadIdx.x / kTpr;
+  const int d0 = ((int)threadIdx.x % kTpr) * kPer;
+  const int64_t chunk_rows = (int64_t)p.n_heads * p.total_q;
+  const int64_t row0 = (int64_t)head * p.total_q + bq.start;
+  float m[kRows], l[kRows], acc[kRows][kPer];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) acc[i][e] = 0.f;
+  }
+  for (int c = 0; c < nch; ++c) {
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      const int row = r0 + kStride * i;
+      if (row < bq.len) {
+        const int64_t prow = c * chunk_rows + row0 + row;
+        const float ls = p.part_lse[prow];
+        float os[kPer];
+        if constexpr (kPer == 4) {
+          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p.part_o + prow * D + d0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) os[e] = v[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < kPer; ++e) os[e] = p.part_o[prow * D + d0 + e];
+        }
+        const float mn = fmaxf(m[i], ls);
+        const float mu = mn == -INFINITY ? 0.f : mn;
+        const float a_old = fast_exp2(m[i] - mu), a_new = fast_exp2(ls - mu);
+        l[i] = l[i] * a_old + a_new;
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) acc[i][e] = acc[i][e] * a_old + a_new * os[e];
+        m[i] = mn;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const int row = r0 + kStride * i;
+    if (row >= bq.len) continue;
+    const float inv = l[i] > 0.f ? 1.f / l[i] : 0.f;
+    uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)(bq.start + row) * p.o_st +
+                    (int64_t)head * p.o_sh + d0;
+    if constexpr (kPer == 4) {
+      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{E::pack2(acc[i][0] * inv, acc[i][1] * inv),
+                                                 E::pack2(acc[i][2] * inv, acc[i][3] * inv)};
+    } else {
+      *reinterpret_cast<uint32_t*>(dst) = E::pack2(acc[i][0] * inv, acc[i][1] * inv);
+    }
+    if (p.lse != nullptr && d0 == 0)
+      p.lse[(int64_t)head * p.lse_sh + bq.start + row] =
+          l[i] > 0.f ? (m[i] + __log2f(l[i])) * kLn2 : -INFINITY;
+  }
+}
+
 template <int D, typename Tag, typename Rel, bool kProj>
 hipError_t launch_prefill_t(const PrefillParams& p_in, hipStream_t stream) {
   PrefillParams p = p_in;
+  if (p.n_chunks < 1) p.n_chunks = 1;
   const int per_tile = p.n_heads * p.batch;
-  const int64_t blocks = (int64_t)p.n_qtiles * per_tile;
+  const int64_t blocks = (int64_t)p.n_qtiles * p.n_chunks * per_tile;
   const int pairs = p.batch * (p.n_heads / p.group);
   p.xcd_pairs = pairs % 8 == 0 ? pairs / 8 : 0;
   if (blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL((prefill_fwd_kernel<D, Tag, Rel, kProj>), dim3((unsigned)blocks),
-                     dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((prefill_fwd_kernel<Shape, D, Tag, Rel, kProj>), dim3((unsigned)blocks),
+                     dim3(Shape::kThreads), 0, stream, p);
+  if (p.chunk_tiles > 0) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((prefill_merge_kernel<Shape, D, Tag>),
+                       dim3(p.n_qtiles * kMergeParts, p.n_heads, p.batch), dim3(kMergeThreads),
+                       0, stream, p);
+  }
   return hipGetLastError();
 }
 
@@ -842,9 +1061,9 @@ hipError_t launch_prefill_rel(const PrefillParams& p, hipStream_t stream) {
 
 }  // namespace
 
-int prefill_block_q() { return kBlockQ; }
-int prefill_block_k() { return kBlockK; }
-int prefill_waves() { return kWaves; }
+int prefill_block_q() { return Shape::kBlockQ; }
+int prefill_block_k() { return Shape::kBlockK; }
+int prefill_waves() { return Shape::kWaves; }
 
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, int qkv_dtype,
                           hipStream_t stream) {

@@ -133,7 +133,12 @@ std::tuple<at::Tensor, at::Tensor> fwd(const at::Tensor& q, const at::Tensor& k,
   }
   check_status(ifa4_validate(&a), "fwd");
   const hipStream_t stream = c10::hip::getCurrentHIPStream(q.device().index()).stream();
-  check_status(ifa4_prefill_fwd(&a, stream), "fwd");
+  // split-KV workspace when the tile table splits this call (0 bytes otherwise)
+  const size_t ws_bytes = ifa4_prefill_workspace_bytes(&a);
+  at::Tensor ws = ws_bytes > 0 ? at::empty({(int64_t)ws_bytes}, q.options().dtype(at::kByte))
+                               : at::Tensor();
+  check_status(ifa4_prefill_fwd_ws(&a, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream),
+               "fwd");
   return {out, lse};
 }
 

@@ -24,6 +24,7 @@ IFA4_FP8_E4M3 = 3
 
 IFA4_FLAG_NO_PRUNE = 0x1
 IFA4_FLAG_BOTTOM_RIGHT = 0x2
+IFA4_FLAG_SPLIT_KV_2 = 0x4
 
 # Every function include/ifa4.h declares: name -> (restype, argtypes).
 _c_int32 = ctypes.c_int32
@@ -91,6 +92,8 @@ SIGNATURES = {
     "ifa4_abi_version": (_c_int32, []),
     "ifa4_validate": (_c_int32, [_P_ARGS]),
     "ifa4_prefill_fwd": (_c_int32, [_P_ARGS, _vp]),
+    "ifa4_prefill_workspace_bytes": (ctypes.c_size_t, [_P_ARGS]),
+    "ifa4_prefill_fwd_ws": (_c_int32, [_P_ARGS, _vp, ctypes.c_size_t, _vp]),
     "ifa4_prefill_tile": (_c_int32, [_P_ARGS, _P_TILE]),
     "ifa4_prefill_rproj_fwd": (_c_int32, [_P_ARGS, ctypes.POINTER(Ifa4RelProj), _vp]),
     "ifa4_prefill_count_tiles": (_c_int32, [_P_ARGS, _P_I32, _P_I32, _P_I64, _P_I64]),

@@ -114,7 +114,7 @@ def inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqle
     by log-sum-exp.  Falls through to the prefill kernel when q holds more
     tokens than there are sequences, or for GQA groups above 16.
 
-    k / v may be torch.float8_e4m3fn (an FP8 KV cache, GQA groups up to 8):
+    k / v may be torch.float8_e4m3fn (an FP8 KV cache, GQA groups up to 16):
     the keys and values are k * k_scale and v * v_scale.
     """
     scale = _resolve(q, k, n_heads, kv_heads, head_dim, softmax_scale)
@@ -122,7 +122,7 @@ def inkling_fa4_rel_attention_decode(q, k, v, rel_logits, cu_seqlens_q, cu_seqle
     group = q.shape[1] // k.shape[1]
     if q.shape[0] != batch or group > 16:
         if k.dtype == torch.float8_e4m3fn:
-            raise ValueError("fp8 K/V needs one query per sequence and GQA groups up to 8")
+            raise ValueError("fp8 K/V needs one query per sequence and GQA groups up to 16")
         return inkling_fa4_rel_attention(q, k, v, rel_logits, cu_seqlens_q, cu_seqlens_k,
                                          max_seqlen_q, max_seqlen_k, rel_extent, causal,
                                          window_size, softmax_scale=scale,

@@ -315,7 +315,8 @@ def test_pruning_bottom_right_visits_exactly_the_tiles_with_visible_pairs(seed):
     ({}, {"k_scale": 0.0}, False, _abi.IFA4_EINVAL),
     ({}, {"v_scale": float("nan")}, False, _abi.IFA4_EINVAL),
     ({}, {"struct_size": 4}, False, _abi.IFA4_EINVAL),
-    ({"n_heads": 16, "kv_heads": 1}, {}, False, _abi.IFA4_EUNSUPPORTED),  # fp8: groups <= 8
+    ({"n_heads": 16, "kv_heads": 1}, {}, False, _abi.IFA4_OK),            # fp8: groups <= 16
+    ({"n_heads": 32, "kv_heads": 1}, {}, False, _abi.IFA4_EUNSUPPORTED),
     ({"k_stride_t": 2 * 128 + 8}, {}, False, _abi.IFA4_EUNSUPPORTED),      # 16-byte fp8 rows
     ({"k_stride_t": 2 * 128 + 16}, {}, False, _abi.IFA4_OK),
     ({"head_dim": 64, "q_stride_h": 64, "k_stride_h": 64, "v_stride_h": 64,

@@ -54,10 +54,11 @@ def test_integration_binding_matches_oracle(cuda, causal, window):
     want = ref_rel_attn(case.q, case.k, case.v, case.rel, case.cu_q, case.cu_k, case.scale,
                         case.rel_extent, causal=causal, window_left=case.window_or_none)
     torch.testing.assert_close(out.cpu().float(), want.float(), atol=ATOL, rtol=RTOL)
-    # the torch binding on the same inputs: same kernel, same bits
+    # the torch binding on the same inputs (it may split the KV range of this
+    # small grid and merge the chunks: equal up to that rounding)
     ref = inkling_fa4_rel_attention(*c.args(), causal=causal, window_size=c.window_size,
                                     softmax_scale=c.scale)
-    assert torch.equal(out, ref)
+    torch.testing.assert_close(out.float(), ref.float(), atol=1e-2, rtol=1e-2)
 
 
 @pytest.mark.gpu
@@ -70,8 +71,10 @@ def test_prefill_cu_seqlens_k_past_total_is_clamped(cuda):
     got, lse = inkling_fa4_rel_attention(c.q, c.k, c.v, c.rel, c.cu_q, bad_k, c.max_q,
                                          c.max_k + 1000, c.rel_extent, causal=False,
                                          softmax_scale=c.scale, return_lse=True)
-    want, want_lse = inkling_fa4_rel_attention(*c.args(), causal=False, softmax_scale=c.scale,
-                                               return_lse=True)
+    # same max_seqlen_k, so that both calls get the same tile plan
+    want, want_lse = inkling_fa4_rel_attention(c.q, c.k, c.v, c.rel, c.cu_q, c.cu_k, c.max_q,
+                                               c.max_k + 1000, c.rel_extent, causal=False,
+                                               softmax_scale=c.scale, return_lse=True)
     torch.cuda.synchronize()
     assert torch.equal(got, want) and torch.equal(lse, want_lse)
 

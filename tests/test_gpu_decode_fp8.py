@@ -87,10 +87,19 @@ def test_fp8_paged_equals_contiguous(cuda, block_size, head_dim):
     _check(got, _oracle(deq))
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_fp8_gqa_group_16(cuda, head_dim):
+    lens = [40, 50, 1000, 4100]
+    case = testing.make_case("fp8_g16", [1] * len(lens), lens, 16, 1, head_dim, torch.bfloat16,
+                             seed=1, causal=False, scale=0.1)
+    got, deq = _fp8_decode(case, cuda)
+    _check(got, _oracle(deq))
+
+
 def test_fp8_rejects_what_it_does_not_serve(cuda):
-    case = testing.make_case("fp8_g16", [1, 1], [40, 50], 16, 1, 128, torch.bfloat16, seed=1,
+    case = testing.make_case("fp8_g32", [1, 1], [40, 50], 32, 1, 128, torch.bfloat16, seed=1,
                              causal=False)
-    with pytest.raises(RuntimeError, match="IFA4_EUNSUPPORTED"):
+    with pytest.raises(ValueError):
         _fp8_decode(case, cuda)
     case = testing.make_case("fp8_prefill", [4], [40], 8, 2, 128, torch.bfloat16, seed=1,
                              causal=False)
