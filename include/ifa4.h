@@ -142,7 +142,8 @@ typedef struct ifa4_tile {
   int32_t block_k;        /* keys per KV tile */
   int32_t waves;          /* wavefronts per workgroup */
   int32_t stages;         /* LDS buffers for K/V */
-  int32_t kv_chunk;       /* decode: most keys one wave streams (0 for prefill) */
+  int32_t kv_chunk;       /* decode: most keys one wave streams; prefill: keys per KV
+                             chunk when ifa4_prefill_fwd_ws splits the call, else 0 */
 } ifa4_tile;
 
 /* Human-readable name of a status code; never NULL. */
@@ -185,7 +186,8 @@ int32_t ifa4_prefill_fwd_ws(const ifa4_args* args, void* workspace, size_t works
 /* Prefill with the fused relative-logit projection (ifa4_rel_proj). */
 int32_t ifa4_prefill_rproj_fwd(const ifa4_args* args, const ifa4_rel_proj* proj, void* stream);
 
-/* Tile shape ifa4_prefill_fwd uses for these arguments. */
+/* Tile shape ifa4_prefill_fwd uses for these arguments, and the KV split of
+ * ifa4_prefill_fwd_ws (kv_chunk). */
 int32_t ifa4_prefill_tile(const ifa4_args* args, ifa4_tile* tile);
 
 /*

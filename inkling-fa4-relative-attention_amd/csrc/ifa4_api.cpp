@@ -337,7 +337,13 @@ int32_t ifa4_prefill_tile(const ifa4_args* args, ifa4_tile* tile) {
       tile->block_k = e.block_k;
       tile->waves = e.waves;
       tile->stages = e.stages;
-      tile->kv_chunk = 0;
+      // split KV (ifa4_prefill_fwd_ws): keys per chunk, 0 when the call does not split
+      const ifa4::PrefillSplit sp = ifa4::prefill_split_for(
+          args->batch, args->n_heads, args->max_seqlen_q, args->max_seqlen_k,
+          args->causal != 0 && (args->flags & IFA4_FLAG_BOTTOM_RIGHT) == 0,
+          (args->flags & IFA4_FLAG_BOTTOM_RIGHT) ? -1 : args->window_left, e.block_q, e.block_k,
+          (args->flags & IFA4_FLAG_SPLIT_KV_2) ? 2 : 0);
+      tile->kv_chunk = sp.chunk_tiles * e.block_k;
       return IFA4_OK;
     }
   }

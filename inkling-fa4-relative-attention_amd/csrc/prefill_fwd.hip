@@ -83,10 +83,10 @@ namespace ifa4 {
 namespace {
 
 // Tile shape of one instantiation of the kernel.
-template <int NQB, int BK, int WPE>
+template <int NQB, int BK, int WPE, int WAVES>
 struct PrefillShape {
   static constexpr int kNqb = NQB;                    // 32-row query blocks per wave
-  static constexpr int kWaves = NQB == 1 ? 4 : 2;     // waves per workgroup
+  static constexpr int kWaves = WAVES;                // waves per workgroup
   static constexpr int kBlockQ = 32 * NQB * kWaves;   // 128
   static constexpr int kBlockK = BK;                  // keys per KV tile (32 or 64)
   static constexpr int kThreads = 64 * kWaves;
@@ -108,9 +108,12 @@ struct PrefillShape {
 #ifndef IFA4_WPE
 #define IFA4_WPE (IFA4_PREFILL_NQB == 1 ? 2 : 1)
 #endif
+#ifndef IFA4_PREFILL_WAVES
+#define IFA4_PREFILL_WAVES (IFA4_PREFILL_NQB == 1 ? 4 : 2)
+#endif
 // The shape the library is built with (sweep knobs IFA4_PREFILL_NQB,
-// IFA4_BLOCK_K, IFA4_WPE).
-using Shape = PrefillShape<IFA4_PREFILL_NQB, IFA4_BLOCK_K, IFA4_WPE>;
+// IFA4_BLOCK_K, IFA4_WPE, IFA4_PREFILL_WAVES).
+using Shape = PrefillShape<IFA4_PREFILL_NQB, IFA4_BLOCK_K, IFA4_WPE, IFA4_PREFILL_WAVES>;
 #ifndef IFA4_LOOK_K
 #define IFA4_LOOK_K 4
 #endif
@@ -353,20 +356,20 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   // Each wave DMAs rows of one tensor (K for the first half of the waves, V for
   // the second).  A lane's offset within a DMA depends on the tile only through
   // kb (added as the scalar offset) and on the block only through the swizzle
-  // phase (blk % kPhases) and a row shift (also scalar): kPhases registers, set once.
-  constexpr int kPhases = 32 / St::kRowsPerDma;  // the swizzle repeats every 32 rows
+  // of its tile row and a row shift (also scalar): one register per DMA of the
+  // wave, set once.
   static_assert(St::kDmaPerWave <= St::kDmaPerTensor && St::kDmaPerTensor % St::kDmaPerWave == 0,
                 "a wave's DMAs stay within one tensor");
-  static_assert(St::kDmaPerWave % kPhases == 0 && St::kDmaPerTensor % kPhases == 0,
-                "a DMA's swizzle phase is its index within the wave's batch");
   const bool dma_v = wave * St::kDmaPerWave >= St::kDmaPerTensor;
   const uint32_t dma_rowb = dma_v ? v_row : k_row;
   const rsrc_t dma_r = dma_v ? rv : rk;
-  uint32_t dma_voff[kPhases];
+  uint32_t dma_voff[St::kDmaPerWave];
 #pragma unroll
-  for (int ph = 0; ph < kPhases; ++ph) {
-    const int row = ph * St::kRowsPerDma + dma_row;
-    dma_voff[ph] = (uint32_t)dma_row * dma_rowb + 16u * (uint32_t)(dma_slot ^ swz<St::kChunks>(row));
+  for (int u = 0; u < St::kDmaPerWave; ++u) {
+    const int id = wave * St::kDmaPerWave + u;
+    const int blk = dma_v ? id - St::kDmaPerTensor : id;
+    const int row = blk * St::kRowsPerDma + dma_row;  // tile row
+    dma_voff[u] = (uint32_t)dma_row * dma_rowb + 16u * (uint32_t)(dma_slot ^ swz<St::kChunks>(row));
   }
   const uint32_t lds_stages = lds_addr(stages);
   auto dma_tile = [&](int kt, uint16_t* stage) {
@@ -379,7 +382,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
       const int blk = dma_v ? id - St::kDmaPerTensor : id;
       const uint32_t soff = (uint32_t)(kb + blk * St::kRowsPerDma) * dma_rowb;
       const uint32_t dst = stage_lds + (uint32_t)(((dma_v ? St::kTile : 0) + blk * 512) * 2);
-      dma_16_so(dma_r, dma_voff[u % kPhases], soff, dst);
+      dma_16_so(dma_r, dma_voff[u], soff, dst);
     }
   };
 #else

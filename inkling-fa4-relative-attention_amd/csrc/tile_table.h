@@ -2,17 +2,20 @@
 // src/inkling_fa4/autotune_configs.py:17-50 (seq-length buckets of
 // BLOCK_Q/BLOCK_K/num_warps/num_stages for sm86/sm90/sm100).
 //
-// Prefill: one shape for every sequence length.  The kernel is written for
-// 4 waves x 32 query rows (BLOCK_Q 128) and 64-key KV tiles in two LDS stages
-// (64 KiB of LDS at head_dim 128, so two workgroups fit in the 160 KiB of a
-// CU; 232 VGPRs, two waves per SIMD); the shape is a compile-time property of
-// the kernel, listed here so the host reports what runs.  Measured on the
-// causal 8 x 4096 workload (profiles/sweep_prefill_knobs_b8_s4096.md): 0.262 ms
-// as listed; 64 rows per wave at one wave per SIMD (PREFILL_NQB 2) 0.469 ms;
-// BLOCK_K 32 and 1-wave-per-SIMD shapes were slower in earlier builds.  The
-// counters there: SQ_VALU_MFMA_BUSY_CYCLES is the same for every variant and
-// GRBM_GUI_ACTIVE follows the time, i.e. the shape sets how much of the MFMA
-// work overlaps the softmax, not how much MFMA work there is.
+// Prefill: one shape for every sequence length, and a sequence-length (grid)
+// dependent split of the KV range (prefill_split_for, below).  The kernel is
+// written for 4 waves x 32 query rows (BLOCK_Q 128) and 64-key KV tiles in two
+// LDS stages (64 KiB of LDS at head_dim 128, so two workgroups fit in the 160
+// KiB of a CU; 236 VGPRs, two waves per SIMD); the shape is a compile-time
+// property of the kernel, listed here so the host reports what runs.  Swept on
+// causal batch 8, Hq 8 / Hkv 2, d 128 at S 1024 / 2048 / 4096 / 8192
+// (profiles/sweep_prefill_shapes_b8.md): BLOCK_K 64 x 4 waves 0.0314 / 0.0771 /
+// 0.2646 / 0.9865 ms; 256-row workgroups of 8 waves +13 / +4.5 / +1.4 / +1.5%;
+// 32-key tiles +9 / +6 / +6 / +6%; 64 rows per wave at one wave per SIMD
+// (PREFILL_NQB 2) +79% at S 4096 (profiles/sweep_prefill_knobs_b8_s4096.md).
+// SQ_VALU_MFMA_BUSY_CYCLES is the same for every variant and GRBM_GUI_ACTIVE
+// follows the time: the shape sets how much of the MFMA work overlaps the
+// softmax, not how much MFMA work there is.
 //
 // Decode: persistent waves of the stream-K pass (at most one per 32-key step).
 #pragma once
@@ -93,7 +96,10 @@ inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seq
 // x 2).
 constexpr int64_t kPrefillSlots = 512;
 constexpr int32_t kPrefillMinChunk = 4;
-constexpr int64_t kPrefillSplitMaxGrid = kPrefillSlots / 4;
+#ifndef IFA4_PREFILL_SPLIT_MAX_GRID
+#define IFA4_PREFILL_SPLIT_MAX_GRID 128
+#endif
+constexpr int64_t kPrefillSplitMaxGrid = IFA4_PREFILL_SPLIT_MAX_GRID;  // kPrefillSlots / 4
 
 struct PrefillSplit {
   int32_t chunk_tiles;  // 0: no split

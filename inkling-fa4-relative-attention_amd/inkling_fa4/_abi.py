@@ -164,9 +164,14 @@ def make_quant(**kw):
     return qt
 
 
-def prefill_tile(head_dim):
+def prefill_tile(head_dim, batch=0, n_heads=1, seq_len=0, causal=True):
+    """Tile shape of the prefill kernel; with a batch of `batch` sequences of
+    `seq_len` tokens over `n_heads` heads, kv_chunk = keys per KV chunk when
+    the tile table splits such a call (0: no split)."""
     t = Ifa4Tile()
-    st = lib().ifa4_prefill_tile(ctypes.byref(make_args(head_dim=head_dim)), ctypes.byref(t))
+    a = make_args(head_dim=head_dim, batch=batch, n_heads=n_heads, kv_heads=1,
+                  max_seqlen_q=seq_len, max_seqlen_k=seq_len, causal=int(causal))
+    st = lib().ifa4_prefill_tile(ctypes.byref(a), ctypes.byref(t))
     if st != IFA4_OK:
         raise ValueError(status_str(st))
     return t

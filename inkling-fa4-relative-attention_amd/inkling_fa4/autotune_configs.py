@@ -37,10 +37,18 @@ def _detect_arch() -> str:
     return name.split(":")[0]
 
 
-def get_preset(seq_len: int, arch: str | None = None, head_dim: int = 128) -> dict:
+def get_preset(seq_len: int, arch: str | None = None, head_dim: int = 128, batch: int = 1,
+               n_heads: int = 4, causal: bool = True) -> dict:
     """Tile config used for `seq_len` query tokens: BLOCK_Q, BLOCK_K,
-    num_warps (wavefronts) and num_stages (LDS buffers).  `arch` is accepted
+    num_warps (wavefronts) and num_stages (LDS buffers), plus KV_CHUNK, the
+    keys per KV chunk when the table splits a causal call of `batch` sequences
+    over `n_heads` heads at that length (0: no split; the defaults are the
+    reference benchmark's batch 1, 4 heads).  The shape is the same at every
+    length (sequence-length buckets were swept and one shape won each); the
+    split is what changes with the length and the grid.  `arch` is accepted
     for signature compatibility; every arch maps to the gfx950 table."""
-    del seq_len, arch
-    bq, bk, w, s = _gfx950_row(head_dim)
-    return {"BLOCK_Q": bq, "BLOCK_K": bk, "num_warps": w, "num_stages": s}
+    del arch
+    t = _abi.prefill_tile(head_dim, batch=batch, n_heads=n_heads, seq_len=seq_len,
+                          causal=causal)
+    return {"BLOCK_Q": t.block_q, "BLOCK_K": t.block_k, "num_warps": t.waves,
+            "num_stages": t.stages, "KV_CHUNK": t.kv_chunk}

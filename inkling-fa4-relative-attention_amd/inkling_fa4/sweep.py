@@ -11,6 +11,8 @@ Two steps, so that variants are built where hipcc is and timed where the GPU is:
   python -m inkling_fa4.sweep build --dir DIR --grid IFA4_LOOK_K=2,4,6 --grid IFA4_PRIO=0,1
   python -m inkling_fa4.sweep run --dir DIR --workload prefill [--seq 4096] [--steps 30]
         [--counters SQ_VALU_MFMA_BUSY_CYCLES,GRBM_GUI_ACTIVE] [--out table.md]
+  python -m inkling_fa4.sweep split [--shapes reference,headline] [--seqs 1024,4096]
+        (split-KV prefill against the unsplit kernel, in-tree build)
 
 `build` writes one sub-directory per grid point holding libifa4.so, a copy of the
 torch binding (it loads the libifa4.so next to it), knobs.json and the digest of
@@ -28,8 +30,12 @@ Knobs (macros of the kernel sources):
                    IFA4_PREFILL_NQB           32-row blocks per wave (1/2)
                    IFA4_BLOCK_K               keys per KV tile (32/64)
                    IFA4_WPE                   waves per SIMD the register budget targets
+                   IFA4_PREFILL_WAVES         waves per workgroup (4: 128 query rows, 8: 256)
+  decode_fwd.hip   IFA4_DECODE_WPE            waves per SIMD the stream pass's registers target
   tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
                    IFA4_DECODE_WAVES_FP8      the same for an fp8 KV cache (workload decode_fp8)
+                   IFA4_DECODE_WAVES_PAGED    the same for a paged cache (workload decode_paged)
+                   IFA4_PREFILL_SPLIT_MAX_GRID  largest prefill grid the table splits (split KV)
 """
 import argparse
 import hashlib
@@ -163,6 +169,78 @@ def cmd_measure(args):
     return 0
 
 
+def _prefill_args(c, out, rel_dtype):
+    """ifa4_args of a prefill call on case `c` (device tensors) writing `out`."""
+    from inkling_fa4 import _abi
+
+    q, k, v, rel = c.q, c.k, c.v, c.rel
+    return _abi.make_args(
+        q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(), rel=rel.data_ptr(), out=out.data_ptr(),
+        cu_seqlens_q=c.cu_q.data_ptr(), cu_seqlens_k=c.cu_k.data_ptr(), q_stride_t=q.stride(0),
+        q_stride_h=q.stride(1), k_stride_t=k.stride(0), k_stride_h=k.stride(1),
+        v_stride_t=v.stride(0), v_stride_h=v.stride(1), rel_stride_t=rel.stride(0),
+        rel_stride_h=rel.stride(1), out_stride_t=out.stride(0), out_stride_h=out.stride(1),
+        total_q=q.shape[0], total_k=k.shape[0], batch=c.cu_q.numel() - 1, n_heads=q.shape[1],
+        kv_heads=k.shape[1], head_dim=q.shape[2], rel_extent=c.rel_extent,
+        rel_width=rel.shape[2], max_seqlen_q=c.max_q, max_seqlen_k=c.max_k,
+        causal=int(c.causal), softmax_scale=c.scale, qkv_dtype=_abi.IFA4_BF16,
+        rel_dtype=rel_dtype)
+
+
+def cmd_split(args):
+    """Split-KV prefill against the unsplit kernel on the same inputs, through
+    the C ABI: ifa4_prefill_fwd (never splits) vs ifa4_prefill_fwd_ws with the
+    workspace the tile table asks for (splits when it decides to).  Shapes:
+    the reference benchmark's (batch 1, Hq = Hkv = 4, per-token bf16 bias of
+    extent 1024) and the headline's (batch 8, Hq 8 / Hkv 2, shared table)."""
+    import ctypes
+
+    import torch
+    from inkling_fa4 import _abi, testing
+
+    lib = _abi.lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rows = ["| shape | seq | workspace MiB | unsplit ms | split ms |", "|---|---|---|---|---|"]
+    for shape in args.shapes.split(","):
+        for seq in (int(x) for x in args.seqs.split(",")):
+            if shape == "reference":
+                case = testing.make_case("reference_config", [seq], [seq], 4, 4, 128,
+                                         torch.bfloat16, seed=7, rel_extent=1024,
+                                         rel_table=False, rel_dtype=torch.bfloat16, rel_std=1.0)
+                rd = _abi.IFA4_BF16
+            else:
+                case = testing.long_prefill(seq, batch=8)
+                rd = _abi.IFA4_FP32
+            c = case.to("cuda")
+            out = torch.empty_like(c.q)
+            a = _prefill_args(c, out, rd)
+            n = lib.ifa4_prefill_workspace_bytes(ctypes.byref(a))
+            ws = torch.empty(max(n, 256), dtype=torch.uint8, device="cuda")
+            times = []
+            for fn in (lambda: lib.ifa4_prefill_fwd(ctypes.byref(a), stream),
+                       lambda: lib.ifa4_prefill_fwd_ws(ctypes.byref(a),
+                                                       ctypes.c_void_p(ws.data_ptr()), n,
+                                                       stream)):
+                t0 = time.perf_counter()
+                while time.perf_counter() - t0 < args.settle:
+                    for _ in range(8):
+                        fn()
+                    torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(args.steps):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1) / args.steps)
+            rows.append(f"| {shape} | {seq} | {n / 2**20:.1f} | {times[0]:.4f} | {times[1]:.4f} |")
+            print(rows[-1], flush=True)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write("\n".join(rows) + "\n")
+    return 0
+
+
 def _counters(db, kernel_prefix):
     con = sqlite3.connect(db)
     rows = con.execute("select kernel_name, counter_name, avg(value) from counters_collection "
@@ -269,8 +347,15 @@ def main(argv=None):
         else:
             r.add_argument("--check-out", default="",
                            help="file for the small-case output ('' = no check case)")
+    sp = sub.add_parser("split")
+    sp.add_argument("--shapes", default="reference,headline")
+    sp.add_argument("--seqs", default="1024,2048,4096,8192")
+    sp.add_argument("--steps", type=int, default=30)
+    sp.add_argument("--settle", type=float, default=0.3)
+    sp.add_argument("--out", default="")
     args = ap.parse_args(argv)
-    return {"build": cmd_build, "run": cmd_run, "measure": cmd_measure}[args.cmd](args)
+    return {"build": cmd_build, "run": cmd_run, "measure": cmd_measure,
+            "split": cmd_split}[args.cmd](args)
 
 
 if __name__ == "__main__":

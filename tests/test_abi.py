@@ -174,9 +174,18 @@ def test_decode_workspace_and_contract():
 def test_tile_table_view():
     t = _abi.prefill_tile(128)
     assert (t.block_q, t.block_k) == (128, 64)
+    assert t.kv_chunk == 0
+    # the reference benchmark's shape (batch 1, 4 heads) splits at S >= 1024 ...
     cfg = autotune_configs.get_preset(4096)
-    assert cfg == {"BLOCK_Q": t.block_q, "BLOCK_K": t.block_k, "num_warps": t.waves,
-                   "num_stages": t.stages}
+    assert {k: cfg[k] for k in ("BLOCK_Q", "BLOCK_K", "num_warps", "num_stages")} == {
+        "BLOCK_Q": t.block_q, "BLOCK_K": t.block_k, "num_warps": t.waves,
+        "num_stages": t.stages}
+    assert cfg["KV_CHUNK"] > 0 and cfg["KV_CHUNK"] % t.block_k == 0
+    assert autotune_configs.get_preset(1024)["KV_CHUNK"] > 0
+    # ... short ones and full grids do not
+    assert autotune_configs.get_preset(64)["KV_CHUNK"] == 0
+    assert autotune_configs.get_preset(4096, batch=8, n_heads=8)["KV_CHUNK"] == 0
+    assert autotune_configs.get_preset(1024, batch=8, n_heads=8)["KV_CHUNK"] == 0
     assert "gfx950" in autotune_configs.PRESETS
     assert autotune_configs._detect_arch().startswith("gfx")
 
