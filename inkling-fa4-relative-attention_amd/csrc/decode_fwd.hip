@@ -51,6 +51,13 @@
 #ifndef IFA4_DECODE_WPE
 #define IFA4_DECODE_WPE 2
 #endif
+// Register buffers of K/V steps in flight per wave for an fp8 cache (the wave
+// computes one step while the loads of the next kNbuf - 1 are outstanding);
+// 16-bit caches use 2 (a third buffer of their twice-larger steps does not fit
+// the register budget).
+#ifndef IFA4_DECODE_NBUF_FP8
+#define IFA4_DECODE_NBUF_FP8 2
+#endif
 
 namespace ifa4 {
 namespace {
@@ -222,7 +229,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   __shared__ __align__(16) uint16_t k_lds[kStep * S::kPitch];
   __shared__ __align__(16) uint16_t v_lds[kStep * D];
   using Q = DecodeQ<D, G>;
-  __shared__ __align__(1024) uint16_t q_lds[2][Q::kElems];
+  constexpr int kNbuf = Eb == 1 ? IFA4_DECODE_NBUF_FP8 : 2;
+  static_assert(kNbuf >= 2 && kNbuf <= 3, "two or three step buffers");
+  // One Q slot per step buffer: the segments of the steps in flight hold
+  // distinct slots, so a slot is rewritten only after its segment's Q was read.
+  __shared__ __align__(1024) uint16_t q_lds[kNbuf][Q::kElems];
 
   const int w = blockIdx.x;
   const int W = p.n_waves;
@@ -535,48 +546,57 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     }
   };
 
-  // ---- stream: loads of step gs+1 in flight while step gs is computed ---------------
-  Cursor ca = locate(g0);
-  if (ca.steps == 0) return;
-  ca.first = true;
-  load_q(ca);
-  u32x4_t ka[S::kLoads], va[S::kLoads], kb[S::kLoads], vb[S::kLoads];
-  load(ka, va, ca);
-  // Next cursor after `cu`, with its Q slot (a new segment takes the other slot,
-  // whose previous segment's Q was read into registers a step earlier).
+  // ---- stream: loads of the next kNbuf - 1 steps in flight while a step is computed --
+  // Buffer j of the ring holds step gs + ((j - j0) mod kNbuf); live[j] says it
+  // holds a step of this wave's range.  Cursors and buffers are indexed by
+  // compile-time constants only (the inner loop is unrolled).
+  Cursor cur[kNbuf];
+  bool live[kNbuf];
+  u32x4_t kbuf[kNbuf][S::kLoads], vbuf[kNbuf][S::kLoads];
+  cur[0] = locate(g0);
+  if (cur[0].steps == 0) return;
+  cur[0].first = true;
+  load_q(cur[0]);
+  load(kbuf[0], vbuf[0], cur[0]);
+  live[0] = true;
+  // Next cursor after `cu`, with its Q slot (a new segment takes the next slot,
+  // whose earlier segment's Q was read into registers kNbuf - 1 steps before).
   auto next = [&](const Cursor& cu, int gs) -> Cursor {
     Cursor nx = locate(gs);
     const bool fresh = nx.seg != cu.seg;
-    nx.slot = fresh ? cu.slot ^ 1 : cu.slot;
+    nx.slot = fresh ? (cu.slot + 1 == kNbuf ? 0 : cu.slot + 1) : cu.slot;
     nx.first = fresh;
     return nx;
   };
+  // issue the loads of step g into buffer j, after the step in buffer jp
+  auto issue = [&](int j, int jp, int g) {
+    live[j] = live[jp] && g < g1;
+    if (live[j]) {
+      cur[j] = next(cur[jp], g);
+      live[j] = cur[j].steps > 0;
+    }
+    if (live[j]) {
+      if (cur[j].first) load_q(cur[j]);
+      load(kbuf[j], vbuf[j], cur[j]);
+    }
+  };
+#pragma unroll
+  for (int j = 1; j < kNbuf - 1; ++j) issue(j, j - 1, g0 + j);
   int gs = g0;
-  while (true) {
-    Cursor cb = ca;
-    bool more1 = gs + 1 < g1;
-    if (more1) {
-      cb = next(ca, gs + 1);
-      more1 = cb.steps > 0;
+  bool more = true;
+  while (more) {
+#pragma unroll
+    for (int j = 0; j < kNbuf; ++j) {
+      if (more) {
+        const int jn = (j + kNbuf - 1) % kNbuf;  // buffer of step gs + kNbuf - 1
+        const int jp = (j + kNbuf - 2) % kNbuf;  // buffer of the step before it
+        issue(jn, jp, gs + kNbuf - 1);
+        const int j1 = (j + 1) % kNbuf;          // buffer of step gs + 1
+        step(kbuf[j], vbuf[j], cur[j], !live[j1] || cur[j1].first);
+        more = live[j1];
+        ++gs;
+      }
     }
-    if (more1) {
-      if (cb.first) load_q(cb);
-      load(kb, vb, cb);
-    }
-    step(ka, va, ca, !more1 || cb.first);
-    if (!more1) break;
-    bool more2 = gs + 2 < g1;
-    if (more2) {
-      ca = next(cb, gs + 2);
-      more2 = ca.steps > 0;
-    }
-    if (more2) {
-      if (ca.first) load_q(ca);
-      load(ka, va, ca);
-    }
-    step(kb, vb, cb, !more2 || ca.first);
-    if (!more2) break;
-    gs += 2;
   }
 }
 
