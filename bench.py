@@ -133,7 +133,10 @@ def prefill_bench(seq_len, steps, warmup, batch=8):
 def prefill_bias_variants(steps, warmup, seq_len=4096, batch=8):
     """The headline shape with the bias from a per-token rel_logits [Tq, Hq, 128]
     fp32 (what the reference operator takes) and from the fused RelLogitsProj
-    factors r [Tq, Hq, 16] fp32, W [16, 128] (no rel_logits in HBM)."""
+    factors r [Tq, Hq, 16], W [16, R'] (no rel_logits in HBM): R' = 128 with
+    fp32 r, and the serving model's global extent 1024 with fp32 and bf16 r,
+    next to the einsum that would materialise its [Tq, Hq, 1024] bf16
+    rel_logits for the per-token path."""
     import torch
     from inkling_fa4 import (inkling_fa4_rel_attention, inkling_fa4_rel_attention_rproj,
                              testing)
@@ -142,15 +145,24 @@ def prefill_bias_variants(steps, warmup, seq_len=4096, batch=8):
                              torch.bfloat16, seed=3, rel_table=False)
     c = case.to("cuda")
     args = c.args()
-    ms_tok = time_gpu(lambda: inkling_fa4_rel_attention(*args, causal=True,
-                                                        softmax_scale=c.scale), steps, warmup)
+    res = {"per_token_rel_ms": time_gpu(lambda: inkling_fa4_rel_attention(
+        *args, causal=True, softmax_scale=c.scale), steps, warmup)}
+    del args
     g = torch.Generator().manual_seed(4)
     r = (0.3 * torch.randn(case.q.shape[0], 8, 16, generator=g)).to("cuda")
-    w = (0.3 * torch.randn(16, 128, generator=g)).to("cuda")
-    ms_proj = time_gpu(lambda: inkling_fa4_rel_attention_rproj(
-        c.q, c.k, c.v, r, w, c.cu_q, c.cu_k, c.max_q, c.max_k, 128, causal=True,
-        softmax_scale=c.scale), steps, warmup)
-    return {"per_token_rel_ms": ms_tok, "rproj_ms": ms_proj}
+    for ext in (128, 1024):
+        w = (0.3 * torch.randn(16, ext, generator=g)).to("cuda")
+        for r_in, key in ((r, f"rproj_rel{ext}_ms"), (r.bfloat16(), f"rproj_rel{ext}_bf16r_ms")):
+            if ext == 128 and r_in.dtype == torch.bfloat16:
+                continue
+            res[key] = time_gpu(lambda: inkling_fa4_rel_attention_rproj(
+                c.q, c.k, c.v, r_in, w, c.cu_q, c.cu_k, c.max_q, c.max_k, ext, causal=True,
+                softmax_scale=c.scale), steps, warmup)
+        if ext == 1024:
+            res["materialise_rel1024_ms"] = time_gpu(
+                lambda: torch.einsum("thc,cd->thd", r, w).to(torch.bfloat16), steps, warmup)
+    res["rproj_ms"] = res["rproj_rel128_ms"]
+    return res
 
 
 # The reference's published prefill latencies (RTX 3090, sm86, after tuning;
@@ -459,7 +471,9 @@ def main():
             result["prefill_sweep"] = sweep
             bv = prefill_bias_variants(max(5, args.steps // 2), max(2, args.warmup // 2), args.seq)
             log(f"prefill seq {args.seq}, per-token bias: {bv['per_token_rel_ms']:.4f} ms; "
-                f"fused RelLogitsProj: {bv['rproj_ms']:.4f} ms")
+                f"fused RelLogitsProj: {bv['rproj_ms']:.4f} ms; at rel_extent 1024: "
+                f"{bv['rproj_rel1024_ms']:.4f} ms (bf16 r {bv['rproj_rel1024_bf16r_ms']:.4f}), "
+                f"materialising its rel_logits: {bv['materialise_rel1024_ms']:.4f} ms")
             result["prefill_bias_variants"] = {k: round(v, 5) for k, v in bv.items()}
             pt = per_token_bias_bench(max(5, args.steps // 2), max(2, args.warmup // 2), 1024,
                                       args.seq)

@@ -126,7 +126,10 @@ typedef struct ifa4_args {
  * applied for 0 <= dist < rel_extent as usual.  r has args.rel_dtype (bf16 or
  * fp32) and the element strides below (last dim contiguous); W is passed
  * transposed, wt = W^T [args.rel_width, 16] fp32, rows contiguous.  args.rel and
- * args.rel_stride_t/h are not read.  rel_extent <= 128 (W^T is staged in LDS).
+ * args.rel_stride_t/h are not read.  Any rel_extent <= rel_width: the band is
+ * projected on the matrix cores (bf16 hi + lo split of r and W^T, ~16
+ * significant bits) one 32-row x 64-key tile at a time; W^T rows are read
+ * from L2 (rel_width x 64 bytes).
  */
 typedef struct ifa4_rel_proj {
   uint32_t struct_size;   /* sizeof(ifa4_rel_proj) */

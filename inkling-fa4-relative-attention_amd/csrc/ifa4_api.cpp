@@ -391,7 +391,6 @@ int32_t ifa4_prefill_rproj_fwd(const ifa4_args* args, const ifa4_rel_proj* pr, v
   if (pr->d_rel != 16) return IFA4_EUNSUPPORTED;
   if (args->rel_dtype != IFA4_BF16 && args->rel_dtype != IFA4_FP32) return IFA4_EUNSUPPORTED;
   if (pr->r_stride_t < 0 || pr->r_stride_h < 0) return IFA4_EINVAL;
-  if (args->rel_extent > 128) return IFA4_EUNSUPPORTED;  // W^T staged in LDS
   // The rel arguments of ifa4_args describe r here: checked below, not by check_args.
   ifa4_args b = *args;
   b.rel = pr->r;
@@ -405,7 +404,8 @@ int32_t ifa4_prefill_rproj_fwd(const ifa4_args* args, const ifa4_rel_proj* pr, v
     if (pr->r == nullptr || pr->wt == nullptr || !aligned(pr->r, esize) || !aligned(pr->wt, 16))
       return IFA4_EINVAL;
     if (pr->r_stride_t != 0 && pr->r_stride_t < 16) return IFA4_EUNSUPPORTED;
-    if (((int64_t)args->max_seqlen_q + 128) * pr->r_stride_t * esize >= (int64_t(1) << 31) ||
+    if (((int64_t)args->max_seqlen_q + ifa4::prefill_proj_block_q()) * pr->r_stride_t * esize >=
+            (int64_t(1) << 31) ||
         (int64_t)args->rel_width * 64 >= (int64_t(1) << 31))
       return IFA4_EUNSUPPORTED;
   }
@@ -414,6 +414,10 @@ int32_t ifa4_prefill_rproj_fwd(const ifa4_args* args, const ifa4_rel_proj* pr, v
   p.rel_st = pr->r_stride_t;
   p.rel_sh = pr->r_stride_h;
   p.wt = args->rel_extent > 0 ? pr->wt : nullptr;  // no bias at all: the plain kernel
+  if (p.wt != nullptr) {
+    const int bq = ifa4::prefill_proj_block_q();
+    p.n_qtiles = (args->max_seqlen_q + bq - 1) / bq;
+  }
   const hipError_t e = ifa4::launch_prefill(p, args->head_dim, args->qkv_dtype,
                                             static_cast<hipStream_t>(stream));
   return e == hipSuccess ? IFA4_OK : IFA4_ELAUNCH;

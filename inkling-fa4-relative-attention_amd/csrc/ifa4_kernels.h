@@ -90,6 +90,7 @@ struct DecodeParams {
 };
 
 int prefill_block_q();
+int prefill_proj_block_q();  // query rows per workgroup of the fused-projection kernel
 int prefill_block_k();
 int prefill_waves();
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, int qkv_dtype, hipStream_t stream);

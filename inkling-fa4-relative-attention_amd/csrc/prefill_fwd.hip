@@ -78,6 +78,12 @@
 #ifndef IFA4_DMA2
 #define IFA4_DMA2 1
 #endif
+#ifndef IFA4_PROJ_SKIP
+#define IFA4_PROJ_SKIP 1
+#endif
+#ifndef IFA4_PROJ_EARLY
+#define IFA4_PROJ_EARLY 1
+#endif
 
 namespace ifa4 {
 namespace {
@@ -165,17 +171,36 @@ constexpr int kLgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);
 constexpr int kBiasLdsMax = 1024;  // longest shared bias table staged in LDS
 
 // Fused relative-logit projection (kProj): bias(i, dist) = sum_c r[i, c] *
-// W[c, dist] with r [Tq, Hq, kProjDim] and W^T [R', kProjDim] fp32.  The
-// workgroup's 128 rows of r (fp32) and the W^T rows of rel_extent <= kWtLdsMax
-// distances are staged in LDS (8 KiB each: with the two 32 KiB K/V stages
-// exactly 80 KiB, two workgroups per CU); 16-byte chunks of row d are swizzled
-// by (d >> 2) & 3 so that 16 lanes reading 16 consecutive rows hit all 64 banks
-// once.  (A W^T read from L2 for longer extents needed ~100 more VGPRs.)
+// W[c, dist] with r [Tq, Hq, kProjDim] and W^T [R', kProjDim] fp32, any
+// rel_extent.  For a wave's 32 rows qa .. qa+31 and a 64-key tile at kb the
+// distances fall in T0 .. T0 + 94, T0 = qa + delta - kb - 63: three blocks of 32
+// distances.  Block T is one MFMA product M^T = W^T[T0 + 32T + m, :] r^T (A =
+// 32 distances x 16 channels, B = 16 channels x 32 rows) in bf16 split into
+// hi + lo parts (W_hi r_hi + W_lo r_hi + W_hi r_lo: ~16 mantissa bits, the lo
+// x lo term is below fp32 rounding of the sum).  The C layout gives lane (u,
+// g) the distances 8i + 4g + j of row u; two blocks go to the wave's tile in
+// LDS (row u, pitch kProjPitch floats), from which the lane holding keys
+// 16h .. 16h+15 of a 32-key block reads its row's 16 distances along a
+// diagonal.  Pitch 68: the 16-byte writes (16 rows per pass) and the diagonal
+// reads (32 rows per pass, row u at u*69 + const) hit distinct banks.  W^T rows
+// of the next tile are fetched with the next tile's DMA.
 constexpr int kProjDim = 16;
-constexpr int kWtLdsMax = 128;
-constexpr int kWtLdsFloats = kWtLdsMax * kProjDim;                   // 2048
-__device__ __forceinline__ int wt_lds_index(int d, int chunk) {
-  return d * kProjDim + 4 * (chunk ^ ((d >> 2) & 3));
+constexpr int kProjPitch = 68;
+// The projection's shape: 8 waves x 32 rows, so that the eight 8.5 KiB
+// projection tiles and the two K/V stages (132 KiB at head_dim 128) give two
+// waves per SIMD from one workgroup per CU.
+using ProjShape = PrefillShape<1, 64, 2, 8>;
+
+// Eight fp32 values -> packed bf16 pairs hi = x truncated (exact in fp32) and
+// lo = bf16(x - hi) (round to nearest even): hi + lo carries 16 significant bits.
+__device__ __forceinline__ void split_bf16x8(const float* x, u32x4_t& hi, u32x4_t& lo) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t a = __float_as_uint(x[2 * k]) & 0xffff0000u;
+    const uint32_t b = __float_as_uint(x[2 * k + 1]) & 0xffff0000u;
+    hi[k] = (a >> 16) | b;
+    lo[k] = Elem<Bf16Tag>::pack2(x[2 * k] - __uint_as_float(a), x[2 * k + 1] - __uint_as_float(b));
+  }
 }
 
 // Bytes a resource over `rows` rows of `stride` elements (row length d) spans.
@@ -231,9 +256,10 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   // constant, which folds into the instruction's offset (one address register
   // per fragment instead of one per fragment and stage).
   __shared__ __align__(1024) uint16_t stages[2 * St::kElems];
-  // bias table (shared-table layout) or, with kProj, the W^T rows and r rows
-  __shared__ __align__(16) float bias_lds[kProj ? kWtLdsFloats : kBiasLdsFloats];
-  __shared__ __align__(16) float r_lds[kProj ? kBlockQ * kProjDim : 4];
+  // bias table (shared-table layout); with kProj, one projection tile per wave
+  __shared__ __align__(16) float bias_lds[kProj ? 4 : kBiasLdsFloats];
+  __shared__ __align__(16) float mproj[kProj ? Sh::kWaves * 32 * kProjPitch : 4];
+  static_assert(!kProj || (kNqb == 1 && kBlockK == 64), "projection tiles: 32 rows x 64 keys");
   uint16_t* const stage0 = stages;
   uint16_t* const stage1 = stages + St::kElems;
 
@@ -411,40 +437,80 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   // Shared-table layout with a table short enough to stage in LDS.
   const bool bias_in_lds =
       !kProj && IFA4_BIAS_LDS && p.rel_st == 0 && rext > 0 && rext <= kBiasLdsMax;
-  // Fused projection: W^T [rel_width, 16] fp32; rel_extent <= kWtLdsMax (host-checked).
-  const bool wt_in_lds = kProj;
+  // Fused projection.  W^T [rel_width, 16] fp32 (64-byte rows) stays in L2;
+  // rows outside [0, rel_extent) read as zero, so the projected bias is zero
+  // there with no further test.  The B operand (this lane's row of r, channels
+  // 8g .. 8g+7 in bf16 hi + lo) is set once; the A operands of a tile (its
+  // three distance blocks) are fetched one tile ahead.
+  using EB = Elem<Bf16Tag>;
   const rsrc_t rwt = make_rsrc(p.wt, kProj ? (uint32_t)((int64_t)p.rel_width * kProjDim * 4) : 0u);
-  // log2(e) * bias of the 16 distances dbase - kc of a 32-key block for this
-  // lane's row (0 outside [0, rext)): the dot product runs over 4-value chunks
-  // of r so that only one chunk of r and one of W^T are live at a time.
-  auto proj_bias = [&](int dbase, int blk, int row, float* bias) {  // row: within the workgroup
+  u32x4_t r_hi{}, r_lo{};
+  u32x4_t w_raw[3][2];
+  // wave-uniform: the tile at kb is visited by this wave and meets the band
+  auto proj_tile = [&](int kb) {
+    return rext > 0 && wrows > 0 && kb < wkend && kb + kBlockK > wkbeg &&
+           qa + wrows - 1 + delta - kb >= 0 && qa + delta - (kb + kBlockK - 1) <= rext - 1;
+  };
+  // distance block t of the tile at kb meets [0, rext) (wave-uniform); blocks
+  // that do not are zero and skip their fetch and products
+  auto proj_live = [&](int kb, int t) {
+    const int lo = qa + delta - kb - (kBlockK - 1) + 32 * t;
+    return !IFA4_PROJ_SKIP || (lo + 31 >= 0 && lo < rext);
+  };
+  auto proj_fetch = [&](int kt) {
+    if (!proj_tile(kt * kBlockK)) return;
+    const int d0 = qa + delta - kt * kBlockK - (kBlockK - 1) + col;  // block 0, row col
 #pragma unroll
-    for (int e = 0; e < 16; ++e) bias[e] = 0.f;
-    if (wt_in_lds) {
-      // four elements at a time; the scheduling barrier keeps the next group's
-      // reads from being hoisted (register pressure of the edge path)
-#pragma unroll
-      for (int eg = 0; eg < 4; ++eg) {
-#pragma unroll
-        for (int ch = 0; ch < kProjDim / 4; ++ch) {
-          const f32x4_t r4 = *reinterpret_cast<const f32x4_t*>(r_lds + wt_lds_index(row, ch));
-#pragma unroll
-          for (int e = 4 * eg; e < 4 * eg + 4; ++e) {
-            const int dist = dbase - (32 * blk + e);
-            const int d = (uint32_t)dist < (uint32_t)rext ? dist : 0;
-            const f32x4_t w = *reinterpret_cast<const f32x4_t*>(bias_lds + wt_lds_index(d, ch));
-#pragma unroll
-            for (int c = 0; c < 4; ++c) bias[e] = fmaf(r4[c], w[c], bias[e]);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int t = 0; t < 3; ++t) {
+      if (!proj_live(kt * kBlockK, t)) continue;
+      const int dist = d0 + 32 * t;
+      const uint32_t off =
+          (uint32_t)dist < (uint32_t)rext ? (uint32_t)dist * 64u + 32u * half : kOutOfRange;
+      w_raw[t][0] = buf_load_16(rwt, off);
+      w_raw[t][1] = buf_load_16(rwt, off + 16);
     }
+  };
+  float* const mp = mproj + (kProj ? wave * 32 * kProjPitch : 0);  // this wave's tile
+  // distance block t of the current tile (its W^T rows split just before use)
+  auto proj_block = [&](int kb, int t) -> f32x16_t {
+    if (!proj_live(kb, t)) return f32x16_t{};
+    float w[8];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int dist = dbase - (32 * blk + e);
-      bias[e] = (uint32_t)dist < (uint32_t)rext ? bias[e] * kLog2e : 0.f;
+    for (int c = 0; c < 4; ++c) {
+      w[c] = __uint_as_float(w_raw[t][0][c]);
+      w[4 + c] = __uint_as_float(w_raw[t][1][c]);
     }
+    u32x4_t w_hi, w_lo;
+    split_bf16x8(w, w_hi, w_lo);
+    f32x16_t acc = EB::mfma32(w_hi, r_hi, f32x16_t{});
+    acc = EB::mfma32(w_lo, r_hi, acc);
+    if constexpr (Rel::kBytes == 4) acc = EB::mfma32(w_hi, r_lo, acc);  // bf16 r: no lo part
+    return acc;
+  };
+  auto proj_put = [&](const f32x16_t& acc, int slot) {
+    float* dst = mp + col * kProjPitch + 32 * slot + 4 * half;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      *reinterpret_cast<f32x4_t*>(dst + 8 * i) =
+          f32x4_t{acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]};
+  };
+  // log2(e) * bias of this lane's 16 keys in key block blk: block blk sees
+  // distance blocks 1 - blk (slot 0) and 2 - blk (slot 1); element e sits at
+  // position col + 31 - 16 * half - e of the lane's row.  Block 1 serves both
+  // key blocks and is projected twice: one accumulator live at a time.
+  auto proj_fill = [&](int kb, int blk) {
+    proj_put(proj_block(kb, 1 - blk), 0);
+    __builtin_amdgcn_sched_barrier(0);
+    proj_put(proj_block(kb, 2 - blk), 1);
+  };
+  // Key block 0's distances are projected before the QK products of the tile
+  // (the LDS writes land while the MFMAs run), key block 1's after its reads.
+  constexpr bool kProjEarly = IFA4_PROJ_EARLY;
+  auto proj_bias = [&](int kb, int blk, float* bias) {
+    if (!(kProjEarly && blk == 0)) proj_fill(kb, blk);
+    const float* src = mp + col * (kProjPitch + 1) + 31 - 16 * half;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) bias[e] = src[-e] * kLog2e;
   };
 
   // Per-token bias of the 16 consecutive keys a lane holds in a 32-key block,
@@ -523,7 +589,16 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
     const int kb = kt * kBlockK;
     // Wave-uniform activity / class of this tile.
     const bool active = wrows > 0 && kb < wkend && kb + kBlockK > wkbeg;
-    if (!active) return;
+    // W^T rows of the next tile (fused projection): fetched once this tile's
+    // are consumed, so that only one tile's operands are live at a time
+    auto fetch_next = [&] {
+      if constexpr (kProj)
+        if (kt + 1 < kt_end) proj_fetch(kt + 1);
+    };
+    if (!active) {
+      fetch_next();
+      return;
+    }
     const int imin = qa, imax = qa + wrows - 1;
     const int jmin = kb, jmax = kb + kBlockK - 1;
     const bool need_mask = jmax >= lk || (p.causal && jmax > imin + qpos) ||
@@ -532,6 +607,9 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
         rext > 0 && (imax + delta - jmin >= 0) && (imin + delta - jmax <= rext - 1);
     const uint16_t* kl = stage;
     const uint16_t* vl = stage + St::kTile;
+    if constexpr (kProj && kProjEarly) {
+      if (has_bias) proj_fill(kb, 0);
+    }
 
     // ---- S^T = K Q^T (each K fragment feeds every row block) ---------------------
     f32x16_t s[kNqb][kBlockK / 32];
@@ -623,7 +701,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
             for (int e = 0; e < 16; ++e) bias[e] = tb[kBlockK - 1 - (32 * blk + e)];
           } else if (has_bias && kProj) {
-            proj_bias(dbase, blk, qi[qb] - q0, bias);
+            proj_bias(kb, blk, bias);
           } else if (has_bias) {
             token_bias(rel_row, dbase - 32 * blk, row_ok[qb], bias);
           }
@@ -651,6 +729,8 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
         mx[qb] = m * c2;
       }
     }
+
+    fetch_next();
 
 #if IFA4_PV2
     if (!vfr_early) {
@@ -826,6 +906,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   // Two barriers per tile: issue tile kt+1's DMA; wait until only it is
   // outstanding for this wave; barrier (every wave's part of tile kt landed);
   // compute; barrier (the stage may be overwritten next).  1.4% slower.
+  static_assert(!kProj, "the projection fetches W^T rows with the one-barrier pipeline");
   auto step = [&](int kt, uint16_t* cur, uint16_t* nxt) {
     if (kt + 1 < kt_end) {
       dma_tile(kt + 1, nxt);
@@ -855,46 +936,18 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
       tab[i] = Rel::load(rrel, off) * kLog2e;
     }
   }
-  // Fused projection: the workgroup's rows of r (fp32) and W^T rows [0, rext)
-  // into LDS (swizzled 16-byte chunks), read with the Q fragments.
-  constexpr int kRPer = kProj ? kBlockQ * kProjDim / 4 / kThreads : 1;  // chunks per thread
-  constexpr int kWtPer = kProj ? kWtLdsFloats / 4 / kThreads : 1;
-  f32x4_t rtab[kRPer], wtab[kWtPer];
+  // Fused projection: this lane's row of r (channels 8 * half .. +7) as the B
+  // operand, and the first tile's W^T rows.
   if constexpr (kProj) {
+    float rv[8];
+    const uint32_t roff = (uint32_t)((qa + col) * (int)p.rel_st + 8 * half) * Rel::kBytes;
 #pragma unroll
-    for (int i = 0; i < kRPer; ++i) {
-      const int idx = tid + i * kThreads;  // row idx / 4 of the workgroup, chunk idx % 4
-      const uint32_t off =
-          (uint32_t)((int64_t)(q0 + (idx >> 2)) * p.rel_st + 4 * (idx & 3)) * Rel::kBytes;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) rtab[i][c] = Rel::load(rrel, off + c * Rel::kBytes);
-    }
-    if (wt_in_lds) {
-#pragma unroll
-      for (int i = 0; i < kWtPer; ++i) {
-        const int idx = tid + i * kThreads;  // W^T row idx / 4, chunk idx % 4
-        const uint32_t off = (idx >> 2) < rext ? (uint32_t)idx * 16 : kOutOfRange;
-        wtab[i] = __builtin_bit_cast(f32x4_t, buf_load_16(rwt, off));
-      }
-    }
+    for (int c = 0; c < 8; ++c) rv[c] = Rel::load(rrel, roff + c * Rel::kBytes);
+    split_bf16x8(rv, r_hi, r_lo);
+    if (kt_beg < kt_end) proj_fetch(kt_beg);
   }
   if (kt_beg < kt_end) dma_tile(kt_beg, stage0);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-  if constexpr (kProj) {
-#pragma unroll
-    for (int i = 0; i < kRPer; ++i) {
-      const int idx = tid + i * kThreads;
-      *reinterpret_cast<f32x4_t*>(r_lds + wt_lds_index(idx >> 2, idx & 3)) = rtab[i];
-    }
-    if (wt_in_lds) {
-#pragma unroll
-      for (int i = 0; i < kWtPer; ++i) {
-        const int idx = tid + i * kThreads;
-        *reinterpret_cast<f32x4_t*>(bias_lds + wt_lds_index(idx >> 2, idx & 3)) = wtab[i];
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(kLgkm0);
-  }
   if (bias_in_lds) {
 #pragma unroll
     for (int i = 0; i < kBiasPer; ++i) {
@@ -1028,7 +1081,7 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillPar
   }
 }
 
-template <int D, typename Tag, typename Rel, bool kProj>
+template <typename Sh, int D, typename Tag, typename Rel, bool kProj>
 hipError_t launch_prefill_t(const PrefillParams& p_in, hipStream_t stream) {
   PrefillParams p = p_in;
   if (p.n_chunks < 1) p.n_chunks = 1;
@@ -1037,12 +1090,12 @@ hipError_t launch_prefill_t(const PrefillParams& p_in, hipStream_t stream) {
   const int pairs = p.batch * (p.n_heads / p.group);
   p.xcd_pairs = pairs % 8 == 0 ? pairs / 8 : 0;
   if (blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL((prefill_fwd_kernel<Shape, D, Tag, Rel, kProj>), dim3((unsigned)blocks),
-                     dim3(Shape::kThreads), 0, stream, p);
+  hipLaunchKernelGGL((prefill_fwd_kernel<Sh, D, Tag, Rel, kProj>), dim3((unsigned)blocks),
+                     dim3(Sh::kThreads), 0, stream, p);
   if (p.chunk_tiles > 0) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((prefill_merge_kernel<Shape, D, Tag>),
+    hipLaunchKernelGGL((prefill_merge_kernel<Sh, D, Tag>),
                        dim3(p.n_qtiles * kMergeParts, p.n_heads, p.batch), dim3(kMergeThreads),
                        0, stream, p);
   }
@@ -1052,19 +1105,20 @@ hipError_t launch_prefill_t(const PrefillParams& p_in, hipStream_t stream) {
 template <int D, typename Tag>
 hipError_t launch_prefill_rel(const PrefillParams& p, hipStream_t stream) {
   if (p.wt != nullptr) {  // fused projection: r in bf16 or fp32
-    return p.rel_dtype == 2 ? launch_prefill_t<D, Tag, RelF32, true>(p, stream)
-                            : launch_prefill_t<D, Tag, RelBf16, true>(p, stream);
+    return p.rel_dtype == 2 ? launch_prefill_t<ProjShape, D, Tag, RelF32, true>(p, stream)
+                            : launch_prefill_t<ProjShape, D, Tag, RelBf16, true>(p, stream);
   }
   switch (p.rel_dtype) {
-    case 0: return launch_prefill_t<D, Tag, RelBf16, false>(p, stream);
-    case 1: return launch_prefill_t<D, Tag, RelF16, false>(p, stream);
-    default: return launch_prefill_t<D, Tag, RelF32, false>(p, stream);
+    case 0: return launch_prefill_t<Shape, D, Tag, RelBf16, false>(p, stream);
+    case 1: return launch_prefill_t<Shape, D, Tag, RelF16, false>(p, stream);
+    default: return launch_prefill_t<Shape, D, Tag, RelF32, false>(p, stream);
   }
 }
 
 }  // namespace
 
 int prefill_block_q() { return Shape::kBlockQ; }
+int prefill_proj_block_q() { return ProjShape::kBlockQ; }
 int prefill_block_k() { return Shape::kBlockK; }
 int prefill_waves() { return Shape::kWaves; }
 

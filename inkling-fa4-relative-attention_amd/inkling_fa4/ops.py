@@ -175,8 +175,10 @@ def inkling_fa4_rel_attention_rproj(q, k, v, rel_r, rel_w, cu_seqlens_q, cu_seql
     materialised.
 
     rel_r [total_q, Hq, 16] (bf16 or fp32, last dim contiguous), rel_w [16, R']
-    with R' >= rel_extent and rel_extent <= 128.  Otherwise as
-    inkling_fa4_rel_attention.
+    with R' >= rel_extent; any rel_extent (the serving model's 512 local and
+    1024 global included).  The band is projected on the matrix cores with
+    r and W split into bf16 hi + lo parts (about 16 significant bits).
+    Otherwise as inkling_fa4_rel_attention.
     """
     scale = _resolve(q, k, None, None, None, softmax_scale)
     if rel_w.dim() != 2 or rel_w.shape[0] != rel_r.shape[-1]:

@@ -10,6 +10,10 @@ Two steps, so that variants are built where hipcc is and timed where the GPU is:
 
   python -m inkling_fa4.sweep build --dir DIR --grid IFA4_LOOK_K=2,4,6 --grid IFA4_PRIO=0,1
   python -m inkling_fa4.sweep run --dir DIR --workload prefill [--seq 4096] [--steps 30]
+        (workloads: prefill = shared bias table; prefill_token = per-token fp32 bias of
+        extent 128; prefill_token1024 = per-token bf16 bias of extent 1024; rproj128 /
+        rproj512 / rproj1024 = fused projection of that extent; decode, decode_fp8,
+        decode_paged)
         [--counters SQ_VALU_MFMA_BUSY_CYCLES,GRBM_GUI_ACTIVE] [--out table.md]
   python -m inkling_fa4.sweep split [--shapes reference,headline] [--seqs 1024,4096]
         (split-KV prefill against the unsplit kernel, in-tree build)
@@ -31,6 +35,10 @@ Knobs (macros of the kernel sources):
                    IFA4_BLOCK_K               keys per KV tile (32/64)
                    IFA4_WPE                   waves per SIMD the register budget targets
                    IFA4_PREFILL_WAVES         waves per workgroup (4: 128 query rows, 8: 256)
+                   IFA4_PROJ_SKIP             fused projection: skip distance blocks outside
+                                              the band (0/1; workloads rproj128/512/1024)
+                   IFA4_PROJ_EARLY            fused projection: key block 0's distances
+                                              projected before the QK products (0/1)
   decode_fwd.hip   IFA4_DECODE_WPE            waves per SIMD the stream pass's registers target
   tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
                    IFA4_DECODE_WAVES_FP8      the same for an fp8 KV cache (workload decode_fp8)
@@ -117,14 +125,37 @@ def _case(workload, seq):
         check = testing.make_case("sweep_check", [700, 64, 33], [700, 64, 33], 8, 2, 128,
                                   torch.bfloat16, seed=2)
         return check, testing.long_prefill(seq, batch=8)
+    if workload.startswith("prefill_token") or workload.startswith("rproj"):
+        # per-token rel_logits (extent 128 fp32, or 1024 bf16 for prefill_token1024),
+        # or the fused projection (its factors are drawn in _call): batch 8,
+        # Hq 8 / Hkv 2, d 128, causal
+        ext = int(workload[5:]) if workload.startswith("rproj") else (
+            1024 if workload == "prefill_token1024" else 128)
+        rd = torch.bfloat16 if workload == "prefill_token1024" else torch.float32
+        mk = lambda name, lens, seed: testing.make_case(  # noqa: E731
+            name, lens, lens, 8, 2, 128, torch.bfloat16, seed=seed, rel_extent=ext,
+            rel_table=False, rel_dtype=rd)
+        return mk("sweep_check", [1300, 64, 33], 2), mk("per_token", [seq] * 8, 3)
     return testing.decode(batch=8, seed=21, causal=False), testing.decode(causal=False)
 
 
 def _call(workload, case, return_lse):
+    import torch
     from inkling_fa4 import (inkling_fa4_rel_attention, inkling_fa4_rel_attention_decode,
-                             inkling_fa4_rel_attention_decode_paged, testing)
+                             inkling_fa4_rel_attention_decode_paged,
+                             inkling_fa4_rel_attention_rproj, testing)
 
-    fn = inkling_fa4_rel_attention if workload == "prefill" else inkling_fa4_rel_attention_decode
+    if workload.startswith("rproj"):  # r [Tq, 8, 16] fp32, W [16, R'] (std 0.3)
+        g = torch.Generator().manual_seed(4)
+        r = (0.3 * torch.randn(case.q.shape[0], case.q.shape[1], 16, generator=g)).to(
+            case.q.device)
+        w = (0.3 * torch.randn(16, case.rel_extent, generator=g)).to(case.q.device)
+        return lambda: inkling_fa4_rel_attention_rproj(
+            case.q, case.k, case.v, r, w, case.cu_q, case.cu_k, case.max_q, case.max_k,
+            case.rel_extent, causal=case.causal, softmax_scale=case.scale,
+            return_lse=return_lse)
+    fn = (inkling_fa4_rel_attention if workload.startswith("prefill")
+          else inkling_fa4_rel_attention_decode)
     args = case.args()
     kw = {}
     if workload == "decode_paged":  # the same keys in blocks of 16, shuffled
@@ -263,7 +294,7 @@ def cmd_run(args):
     if len(sources) > 1:
         print(f"warning: variants were built from different sources {sorted(sources)}",
               file=sys.stderr, flush=True)
-    kernel = "prefill_fwd_kernel" if args.workload == "prefill" else "decode_stream_kernel"
+    kernel = "decode_stream_kernel" if args.workload.startswith("decode") else "prefill_fwd_kernel"
     rows, ref = [], None
     with tempfile.TemporaryDirectory() as tmp:
         for name, d, knobs in variants:
@@ -333,7 +364,9 @@ def main(argv=None):
     b.add_argument("--jobs", type=int, default=4)
     for name in ("run", "measure"):
         r = sub.add_parser(name)
-        r.add_argument("--workload", choices=["prefill", "decode", "decode_fp8", "decode_paged"],
+        r.add_argument("--workload", choices=["prefill", "prefill_token", "prefill_token1024",
+                                              "rproj128", "rproj512", "rproj1024", "decode",
+                                              "decode_fp8", "decode_paged"],
                        default="prefill")
         r.add_argument("--seq", type=int, default=4096)
         r.add_argument("--steps", type=int, default=30)

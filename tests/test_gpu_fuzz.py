@@ -132,7 +132,7 @@ def test_decode_fp8_random_configs(cuda, seed):
 def test_rproj_random_configs(cuda, seed):
     lens_q, lens_k, hq, hkv, d, dtype, opts, br = _draw(5000 + seed, decode=False)
     r = random.Random(seed)
-    opts["rel_extent"] = r.choice([1, 16, 64, 100, 128])
+    opts["rel_extent"] = r.choice([1, 16, 64, 100, 128, 300, 512, 1024])
     width = opts["rel_extent"] + r.choice([0, 9])
     opts["rel_width"] = width
     case = testing.make_case(f"fuzzr{seed}", lens_q, lens_k, hq, hkv, d, dtype, seed=seed, **opts)

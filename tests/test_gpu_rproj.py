@@ -1,6 +1,8 @@
 """GPU parity of prefill with the fused relative-logit projection
 (inkling_fa4_rel_attention_rproj): the bias is computed in the kernel from
-r [Tq, Hq, 16] and W [16, R'] instead of a materialised rel_logits.
+r [Tq, Hq, 16] and W [16, R'] instead of a materialised rel_logits, on the
+matrix cores, for any rel_extent (128 and below, and the serving model's 512
+and 1024).
 
 Against the oracle on the einsum-materialised rel_logits: out within atol /
 rtol 2e-2, lse within 1e-3.  A rank-one factorisation that reproduces a
@@ -95,9 +97,36 @@ def test_rproj_rank_one_equals_table_path(cuda):
     torch.testing.assert_close(got[1], lse.cpu(), atol=1e-5, rtol=0)
 
 
-def test_rproj_rejects_long_extent(cuda):
-    case = testing.make_case("rproj_long", [64], [64], 4, 4, 64, torch.bfloat16, seed=1,
-                             rel_extent=256, rel_width=256)
-    r, w = _factors(case, 256, seed=1)
-    with pytest.raises(RuntimeError, match="IFA4_EUNSUPPORTED"):
-        _run(case, r, w, cuda)
+@pytest.mark.parametrize("r_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rel_extent", [512, 1024])
+def test_rproj_serving_extents(cuda, r_dtype, rel_extent):
+    """The serving model's local (512) and global (1024) extents
+    (outputs/architecture.md:57-58): sequences shorter than the band, across
+    it and longer than it; 256-row query tiles with ragged tails."""
+    lens = [1500, 700, 64, 1100, 2100]
+    case = testing.make_case("rproj_serving", lens, lens, 8, 2, 128, torch.bfloat16, seed=44,
+                             rel_extent=rel_extent, rel_width=rel_extent + 16)
+    r, w = _factors(case, rel_extent + 16, seed=rel_extent, r_dtype=r_dtype)
+    _check(_run(case, r, w, cuda), _oracle(case, r, w))
+
+
+@pytest.mark.parametrize("causal,window,bottom_right", [(True, 700, False), (False, -1, True),
+                                                        (True, -1, True)])
+def test_rproj_long_extent_masks(cuda, causal, window, bottom_right):
+    """rel_extent 1024 with a window, bottom-right chunked prefill (300 new
+    tokens over 1800 keys) and lq > lk."""
+    case = testing.make_case("rproj_masks", [300, 1200, 900], [1800, 1200, 600], 6, 3, 64,
+                             torch.float16, seed=45, causal=causal, window_left=window,
+                             rel_extent=1024, rel_width=1024)
+    r, w = _factors(case, 1024, seed=5)
+    _check(_run(case, r, w, cuda, bottom_right), _oracle(case, r, w, bottom_right))
+
+
+def test_rproj_large_bias_lse(cuda):
+    """Bias values of several units (r, W std 1): the hi + lo split keeps the
+    projected bias to ~2^-16 relative, so the LSE stays within 1e-3."""
+    lens = [1024, 513]
+    case = testing.make_case("rproj_big", lens, lens, 4, 4, 128, torch.bfloat16, seed=46,
+                             rel_extent=1024, rel_width=1024)
+    r, w = _factors(case, 1024, seed=6, std=1.0)
+    _check(_run(case, r, w, cuda), _oracle(case, r, w))
