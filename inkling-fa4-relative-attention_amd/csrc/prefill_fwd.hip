@@ -401,7 +401,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   auto dma_tile = [&](int kt, uint16_t* stage) {
     const int kb = kt * kBlockK;
     const uint32_t stage_lds = lds_stages + (uint32_t)((stage - stages) * 2);
-    hazard_nop5();
+    if (!IFA4_DMA_COVER_EACH) hazard_nop5();  // batch cover (sweep knob)
 #pragma unroll
     for (int u = 0; u < St::kDmaPerWave; ++u) {
       const int id = wave * St::kDmaPerWave + u;

@@ -39,6 +39,8 @@ Knobs (macros of the kernel sources):
                                               the band (0/1; workloads rproj128/512/1024)
                    IFA4_PROJ_EARLY            fused projection: key block 0's distances
                                               projected before the QK products (0/1)
+  ifa4_device.hpp  IFA4_DMA_COVER_EACH        hazard cover on every LDS DMA (1) or one per
+                                              batch of a tile's DMAs (0)
   decode_fwd.hip   IFA4_DECODE_WPE            waves per SIMD the stream pass's registers target
   tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
                    IFA4_DECODE_WAVES_FP8      the same for an fp8 KV cache (workload decode_fp8)
@@ -120,10 +122,11 @@ def _case(workload, seq):
     from inkling_fa4 import testing
 
     if workload == "prefill":
-        # check case: ragged tails, diagonal and bias-band tiles, and a run of
-        # interior tiles (the 700-token sequence)
-        check = testing.make_case("sweep_check", [700, 64, 33], [700, 64, 33], 8, 2, 128,
-                                  torch.bfloat16, seed=2)
+        # check case: ragged tails, bias-band tiles, a run of interior tiles (the
+        # 700-token sequence), Lq > Lk and Lq < Lk; non-causal, so that no mask
+        # hides a bias element (the timed case is causal)
+        check = testing.make_case("sweep_check", [700, 64, 300], [700, 33, 500], 8, 2, 128,
+                                  torch.bfloat16, seed=2, causal=False, rel_extent=400)
         return check, testing.long_prefill(seq, batch=8)
     if workload.startswith("prefill_token") or workload.startswith("rproj"):
         # per-token rel_logits (extent 128 fp32, or 1024 bf16 for prefill_token1024),
