@@ -1003,9 +1003,9 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
 // workgroups per (q tile, head, sequence), each a quarter of the tile's rows; a
 // tile whose range did not split was written by the prefill kernel itself and
 // is skipped.  32 threads share a row (head_dim / 32 consecutive d values each)
-// and a thread holds kRows rows; the chunks are the outer loop, so each thread
-// has kRows independent loads in flight per chunk while it merges online
-// (running max over the chunks' LSEs).
+// and a thread holds kRows rows; chunks go in rounds of kChunkBatch whose loads
+// (rows x chunks) are all in flight at once, merged online (running max over
+// the chunks' LSEs).
 constexpr int kMergeThreads = 256;
 constexpr int kMergeParts = 4;
 template <typename Sh, int D, typename Tag>
@@ -1036,30 +1036,49 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillPar
 #pragma unroll
     for (int e = 0; e < kPer; ++e) acc[i][e] = 0.f;
   }
-  for (int c = 0; c < nch; ++c) {
+  // kChunkBatch chunks per round: every load of a round (its rows x chunks)
+  // is issued before the first is used
+  constexpr int kChunkBatch = 4;
+  for (int c0 = 0; c0 < nch; c0 += kChunkBatch) {
+    float ls[kChunkBatch][kRows];
+    float os[kChunkBatch][kRows][kPer];
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) {
-      const int row = r0 + kStride * i;
-      if (row < bq.len) {
-        const int64_t prow = c * chunk_rows + row0 + row;
-        const float ls = p.part_lse[prow];
-        float os[kPer];
+    for (int cb = 0; cb < kChunkBatch; ++cb) {
+#pragma unroll
+      for (int i = 0; i < kRows; ++i) {
+        const int row = r0 + kStride * i;
+        const bool ok = row < bq.len && c0 + cb < nch;
+        const int64_t prow = (c0 + cb) * chunk_rows + row0 + row;
+        ls[cb][i] = ok ? p.part_lse[prow] : -INFINITY;
         if constexpr (kPer == 4) {
-          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p.part_o + prow * D + d0);
+          const f32x4_t v =
+              ok ? *reinterpret_cast<const f32x4_t*>(p.part_o + prow * D + d0) : f32x4_t{};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) os[e] = v[e];
+          for (int e = 0; e < 4; ++e) os[cb][i][e] = v[e];
         } else {
 #pragma unroll
-          for (int e = 0; e < kPer; ++e) os[e] = p.part_o[prow * D + d0 + e];
+          for (int e = 0; e < kPer; ++e) os[cb][i][e] = ok ? p.part_o[prow * D + d0 + e] : 0.f;
         }
-        const float mn = fmaxf(m[i], ls);
-        const float mu = mn == -INFINITY ? 0.f : mn;
-        const float a_old = fast_exp2(m[i] - mu), a_new = fast_exp2(ls - mu);
-        l[i] = l[i] * a_old + a_new;
-#pragma unroll
-        for (int e = 0; e < kPer; ++e) acc[i][e] = acc[i][e] * a_old + a_new * os[e];
-        m[i] = mn;
       }
+    }
+#pragma unroll
+    for (int i = 0; i < kRows; ++i) {
+      float mn = m[i];
+#pragma unroll
+      for (int cb = 0; cb < kChunkBatch; ++cb) mn = fmaxf(mn, ls[cb][i]);
+      const float mu = mn == -INFINITY ? 0.f : mn;
+      const float a_old = fast_exp2(m[i] - mu);
+      l[i] *= a_old;
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) acc[i][e] *= a_old;
+#pragma unroll
+      for (int cb = 0; cb < kChunkBatch; ++cb) {
+        const float a_new = fast_exp2(ls[cb][i] - mu);
+        l[i] += a_new;
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) acc[i][e] += a_new * os[cb][i][e];
+      }
+      m[i] = mn;
     }
   }
 #pragma unroll
@@ -1092,12 +1111,14 @@ hipError_t launch_prefill_t(const PrefillParams& p_in, hipStream_t stream) {
   if (blocks <= 0) return hipSuccess;
   hipLaunchKernelGGL((prefill_fwd_kernel<Sh, D, Tag, Rel, kProj>), dim3((unsigned)blocks),
                      dim3(Sh::kThreads), 0, stream, p);
-  if (p.chunk_tiles > 0) {
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((prefill_merge_kernel<Sh, D, Tag>),
-                       dim3(p.n_qtiles * kMergeParts, p.n_heads, p.batch), dim3(kMergeThreads),
-                       0, stream, p);
+  if constexpr (!kProj) {  // the fused projection never splits
+    if (p.chunk_tiles > 0) {
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL((prefill_merge_kernel<Sh, D, Tag>),
+                         dim3(p.n_qtiles * kMergeParts, p.n_heads, p.batch), dim3(kMergeThreads),
+                         0, stream, p);
+    }
   }
   return hipGetLastError();
 }

@@ -10,7 +10,9 @@ Two steps, so that variants are built where hipcc is and timed where the GPU is:
 
   python -m inkling_fa4.sweep build --dir DIR --grid IFA4_LOOK_K=2,4,6 --grid IFA4_PRIO=0,1
   python -m inkling_fa4.sweep run --dir DIR --workload prefill [--seq 4096] [--steps 30]
-        (workloads: prefill = shared bias table; prefill_token = per-token fp32 bias of
+        (workloads: prefill = shared bias table; prefill_reference = the reference's own
+        benchmark config (batch 1, 4 heads, per-token bf16 bias of extent 1024, split
+        KV); prefill_token = per-token fp32 bias of
         extent 128; prefill_token1024 = per-token bf16 bias of extent 1024; rproj128 /
         rproj512 / rproj1024 = fused projection of that extent; decode, decode_fp8,
         decode_paged)
@@ -128,6 +130,14 @@ def _case(workload, seq):
         check = testing.make_case("sweep_check", [700, 64, 300], [700, 33, 500], 8, 2, 128,
                                   torch.bfloat16, seed=2, causal=False, rel_extent=400)
         return check, testing.long_prefill(seq, batch=8)
+    if workload == "prefill_reference":
+        # the reference's benchmark config (benchmarks/benchmark_prefill.py:20-49):
+        # batch 1, Hq = Hkv = 4, d 128, causal, per-token bf16 bias of extent 1024;
+        # the tile table splits its KV range (underfilled grid)
+        mk = lambda name, lens, seed: testing.make_case(  # noqa: E731
+            name, lens, lens, 4, 4, 128, torch.bfloat16, seed=seed, rel_extent=1024,
+            rel_table=False, rel_dtype=torch.bfloat16, rel_std=1.0)
+        return mk("sweep_check", [1500], 2), mk("reference_config", [seq], 7)
     if workload.startswith("prefill_token") or workload.startswith("rproj"):
         # per-token rel_logits (extent 128 fp32, or 1024 bf16 for prefill_token1024),
         # or the fused projection (its factors are drawn in _call): batch 8,
@@ -367,7 +377,8 @@ def main(argv=None):
     b.add_argument("--jobs", type=int, default=4)
     for name in ("run", "measure"):
         r = sub.add_parser(name)
-        r.add_argument("--workload", choices=["prefill", "prefill_token", "prefill_token1024",
+        r.add_argument("--workload", choices=["prefill", "prefill_reference", "prefill_token",
+                                              "prefill_token1024",
                                               "rproj128", "rproj512", "rproj1024", "decode",
                                               "decode_fp8", "decode_paged"],
                        default="prefill")
