@@ -81,25 +81,34 @@ inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seq
 }
 
 // Split KV for prefill calls whose grid leaves the chip underfilled (few
-// sequences or heads, short sequences): when the grid holds at most a quarter
-// of the resident workgroup slots and the longest query tile's KV range exceeds
-// the work one slot would get with perfect balance, every query tile's range is
-// cut into chunks of that many tiles (at least kPrefillMinChunk), one workgroup
-// per chunk, and a second pass merges the chunks' partials by log-sum-exp.
-// Measured (one sequence, Hq = Hkv = 4, per-token bias of extent 1024): S 1024
-// 65.5 -> 46.1 us, S 2048 87.2 -> 70.0, S 4096 120.7 -> 114.9; a fuller grid
-// loses more to the partials' HBM traffic than it gains (batch 8 x 1024, 512
-// workgroups: 32.0 -> 52.7 us).  The estimate assumes every sequence holds
-// max_seqlen_q queries over max_seqlen_k keys (top-left); it only steers
-// performance, any chunk size gives the same results up to rounding.
-// kPrefillSlots: resident workgroups of the prefill kernel on MI355X (256 CUs
-// x 2).
+// sequences or heads, short sequences): the longest query tile's KV range is
+// the critical path, so when it exceeds the work one slot would get with
+// perfect balance, every query tile's range is cut into chunks of that many
+// tiles (at least kPrefillMinChunk), one workgroup per chunk, and a second pass
+// merges the chunks' partials by log-sum-exp.  Where it pays (same-session
+// sweeps, per-token bf16 bias of extent 1024, Hq = Hkv, causal):
+//   * grids of at most a quarter of the resident slots always: one sequence
+//     over 4 heads, S 1024 / 2048 / 4096: 45.4 -> 22.2, 71.9 -> 31.3,
+//     104.9 -> 65.8 us;
+//   * grids of up to half of them when the longest range is at least
+//     kPrefillSplitWideMinTiles: batch 8 x 1024 over 4 heads (256 workgroups,
+//     16 tiles) 53.4 -> 43.3 us, 4 x 2048 73.1 -> 63.7, 1 x 8192 172.5 -> 147.7;
+//     with 8-tile ranges the merge costs more than it saves (16 x 512: 30.6 ->
+//     31.9 us; the shared-table 8 x 512 over 8 heads: 18.0 -> 28.8);
+//   * never above: every grid of 512 workgroups measured lost (8 x 1024 over 8
+//     heads 32.0 -> 45.6 us, 1 x 16384 over 4 heads 373 -> 447, 2 x 8192 206 -> 225).
+// The estimate assumes every sequence holds max_seqlen_q queries over
+// max_seqlen_k keys (top-left); it only steers performance, any chunk size
+// gives the same results up to rounding.  kPrefillSlots: resident workgroups
+// of the prefill kernel on MI355X (256 CUs x 2).
 constexpr int64_t kPrefillSlots = 512;
 constexpr int32_t kPrefillMinChunk = 4;
 #ifndef IFA4_PREFILL_SPLIT_MAX_GRID
-#define IFA4_PREFILL_SPLIT_MAX_GRID 128
+#define IFA4_PREFILL_SPLIT_MAX_GRID 256
 #endif
-constexpr int64_t kPrefillSplitMaxGrid = IFA4_PREFILL_SPLIT_MAX_GRID;  // kPrefillSlots / 4
+constexpr int64_t kPrefillSplitMaxGrid = IFA4_PREFILL_SPLIT_MAX_GRID;  // kPrefillSlots / 2
+constexpr int64_t kPrefillSplitSmallGrid = 128;                        // kPrefillSlots / 4
+constexpr int64_t kPrefillSplitWideMinTiles = 16;
 
 struct PrefillSplit {
   int32_t chunk_tiles;  // 0: no split
@@ -134,6 +143,7 @@ inline PrefillSplit prefill_split_for(int64_t batch, int64_t n_heads, int64_t ma
   if (chunk <= 0) {
     const int64_t grid = (max_q + block_q - 1) / block_q * n_heads * batch;
     if (grid > kPrefillSplitMaxGrid) return s;
+    if (grid > kPrefillSplitSmallGrid && tmax < kPrefillSplitWideMinTiles) return s;
     const int64_t balanced = (total * batch * n_heads + kPrefillSlots - 1) / kPrefillSlots;
     chunk = balanced > kPrefillMinChunk ? balanced : kPrefillMinChunk;
     if (tmax <= chunk) return s;

@@ -119,7 +119,7 @@ def cmd_build(args):
     return 0
 
 
-def _case(workload, seq):
+def _case(workload, seq, batch=1, heads=4):
     import torch
     from inkling_fa4 import testing
 
@@ -134,10 +134,11 @@ def _case(workload, seq):
         # the reference's benchmark config (benchmarks/benchmark_prefill.py:20-49):
         # batch 1, Hq = Hkv = 4, d 128, causal, per-token bf16 bias of extent 1024;
         # the tile table splits its KV range (underfilled grid)
-        mk = lambda name, lens, seed: testing.make_case(  # noqa: E731
-            name, lens, lens, 4, 4, 128, torch.bfloat16, seed=seed, rel_extent=1024,
+        # (--batch / --heads change the batch and the head count, Hq = Hkv)
+        mk = lambda name, lens, h, seed: testing.make_case(  # noqa: E731
+            name, lens, lens, h, h, 128, torch.bfloat16, seed=seed, rel_extent=1024,
             rel_table=False, rel_dtype=torch.bfloat16, rel_std=1.0)
-        return mk("sweep_check", [1500], 2), mk("reference_config", [seq], 7)
+        return mk("sweep_check", [1500], 4, 2), mk("reference_config", [seq] * batch, heads, 7)
     if workload.startswith("prefill_token") or workload.startswith("rproj"):
         # per-token rel_logits (extent 128 fp32, or 1024 bf16 for prefill_token1024),
         # or the fused projection (its factors are drawn in _call): batch 8,
@@ -190,7 +191,7 @@ def cmd_measure(args):
     """Child process: small-case output to args.check_out, then the timing (JSON)."""
     import torch
 
-    small, big = (c.to("cuda") for c in _case(args.workload, args.seq))
+    small, big = (c.to("cuda") for c in _case(args.workload, args.seq, args.batch, args.heads))
     if args.check_out:  # skipped under counters: only the timed workload's dispatches count
         out, lse = _call(args.workload, small, True)()
         torch.save({"out": out.cpu(), "lse": lse.cpu()}, args.check_out)
@@ -317,7 +318,8 @@ def cmd_run(args):
                 env["IFA4_LIB_DIR"] = os.path.abspath(d)
             check = os.path.join(tmp, f"{name}.pt")
             child = [sys.executable, "-m", "inkling_fa4.sweep", "measure", "--workload",
-                     args.workload, "--seq", str(args.seq), "--steps", str(args.steps),
+                     args.workload, "--seq", str(args.seq), "--batch", str(args.batch),
+                     "--heads", str(args.heads), "--steps", str(args.steps),
                      "--warmup", str(args.warmup), "--settle", str(args.settle),
                      "--check-out", check]
             res = subprocess.run(child, env=env, cwd=_PKG_ROOT, capture_output=True, text=True,
@@ -383,6 +385,9 @@ def main(argv=None):
                                               "decode_fp8", "decode_paged"],
                        default="prefill")
         r.add_argument("--seq", type=int, default=4096)
+        r.add_argument("--batch", type=int, default=1,
+                       help="prefill_reference: sequences of --seq tokens")
+        r.add_argument("--heads", type=int, default=4, help="prefill_reference: Hq = Hkv")
         r.add_argument("--steps", type=int, default=30)
         r.add_argument("--warmup", type=int, default=5)
         r.add_argument("--settle", type=float, default=0.5, help="seconds of untimed calls first")

@@ -102,6 +102,13 @@ def test_split_plan_on_the_host():
     assert lib.ifa4_prefill_fwd_ws(ctypes.byref(a), 1 << 20, n - 1, None) == _abi.IFA4_EWORKSPACE
     # short sequences never split (a single KV tile per query tile)
     assert _workspace_bytes(1, 4, 4, 64)[0] == 0
+    # grids of up to half the resident slots split only with long KV ranges:
+    # 256 workgroups with 16-tile ranges split, with 8-tile ranges not
+    assert _workspace_bytes(8, 4, 4, 1024)[0] > 0
+    assert _workspace_bytes(16, 4, 4, 512)[0] == 0
+    assert _workspace_bytes(8, 8, 2, 512)[0] == 0
+    # 512 workgroups never split
+    assert _workspace_bytes(1, 4, 4, 16384)[0] == 0
     # the test flag splits everything with more than two tiles per query tile
     assert _workspace_bytes(8, 8, 2, 4096, flags=SPLIT2)[0] > 0
 
