@@ -18,11 +18,22 @@ def _gfx950_row(head_dim=128):
     return (t.block_q, t.block_k, t.waves, t.stages)
 
 
+# Sequence lengths the shape was swept at (causal batch 8, Hq 8 / Hkv 2, d 128;
+# timing plus SQ_VALU_MFMA_BUSY_CYCLES / GRBM_GUI_ACTIVE per variant): the same
+# shape (64-key tiles, 4 waves x 32 rows) was fastest at each of them, so every
+# bucket holds it; what changes with the length and the grid is the KV split
+# (get_preset's KV_CHUNK).
+SWEPT_SEQ_LENS = (1024, 2048, 4096, 8192)
+
+
 def __getattr__(name):
-    # PRESETS is built on first access (it queries libifa4.so).
+    # PRESETS is built on first access (it queries libifa4.so), in the
+    # reference's layout: (threshold, BLOCK_Q, BLOCK_K, num_warps, num_stages)
+    # buckets, the last used above the largest threshold.
     if name == "PRESETS":
         bq, bk, w, st = _gfx950_row(128)
-        return {"gfx950": {"default": (bq, bk, w, st), "buckets": []}}
+        return {"gfx950": {"default": (bq, bk, w, st),
+                           "buckets": [(s, bq, bk, w, st) for s in SWEPT_SEQ_LENS]}}
     raise AttributeError(name)
 
 

@@ -186,7 +186,12 @@ def test_tile_table_view():
     assert autotune_configs.get_preset(64)["KV_CHUNK"] == 0
     assert autotune_configs.get_preset(4096, batch=8, n_heads=8)["KV_CHUNK"] == 0
     assert autotune_configs.get_preset(1024, batch=8, n_heads=8)["KV_CHUNK"] == 0
-    assert "gfx950" in autotune_configs.PRESETS
+    presets = autotune_configs.PRESETS["gfx950"]
+    # the reference's layout: (threshold, BLOCK_Q, BLOCK_K, num_warps, num_stages)
+    # buckets at the swept lengths, each holding the shape get_preset reports
+    assert [b[0] for b in presets["buckets"]] == [1024, 2048, 4096, 8192]
+    for b in presets["buckets"]:
+        assert b[1:] == presets["default"] == (t.block_q, t.block_k, t.waves, t.stages)
     assert autotune_configs._detect_arch().startswith("gfx")
 
 
