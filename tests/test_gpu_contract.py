@@ -1,9 +1,10 @@
 """The boundary's contract, end to end.
 
-* The ctypes binding that INTEGRATION.md shows a maintainer adding on the
-  reference side (`prefill_via_c_abi`) is taken verbatim from that file,
-  executed, and its output compared with the oracle (out atol/rtol 2e-2):
-  the documented binding is the tested one.
+* The ctypes bindings that INTEGRATION.md shows a maintainer adding on the
+  reference side (`prefill_via_c_abi`, `decode_via_c_abi` with its workspace)
+  are taken verbatim from that file, executed, and their output compared with
+  the oracle (out atol/rtol 2e-2, lse 1e-3): the documented bindings are the
+  tested ones.
 * cu_seqlens are read only on the device, where each sequence's range is
   clamped to the tensors' rows (include/ifa4.h).  A cu_seqlens_k whose last
   offset runs past total_k gives exactly the result of the clamped array, and
@@ -24,20 +25,21 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ATOL, RTOL, LSE_ATOL = 2e-2, 2e-2, 1e-3
 
 
-def _integration_binding():
-    """The python block of INTEGRATION.md that defines prefill_via_c_abi, executed."""
+def _integration_binding(name="prefill_via_c_abi"):
+    """The python block of INTEGRATION.md that defines `name`, executed."""
     with open(os.path.join(REPO, "INTEGRATION.md")) as f:
         text = f.read()
     blocks = [b for b in re.findall(r"```python\n(.*?)```", text, re.S)
-              if "def prefill_via_c_abi" in b]
-    assert len(blocks) == 1, "INTEGRATION.md holds one prefill_via_c_abi binding"
+              if f"def {name}" in b]
+    assert len(blocks) == 1, f"INTEGRATION.md holds one {name} binding"
     ns = {}
-    exec(compile(blocks[0], "INTEGRATION.md:prefill_via_c_abi", "exec"), ns)
-    return ns["prefill_via_c_abi"]
+    exec(compile(blocks[0], f"INTEGRATION.md:{name}", "exec"), ns)
+    return ns[name]
 
 
 def test_integration_binding_compiles():
     assert callable(_integration_binding())
+    assert callable(_integration_binding("decode_via_c_abi"))
 
 
 @pytest.mark.gpu
@@ -59,6 +61,24 @@ def test_integration_binding_matches_oracle(cuda, causal, window):
     ref = inkling_fa4_rel_attention(*c.args(), causal=causal, window_size=c.window_size,
                                     softmax_scale=c.scale)
     torch.testing.assert_close(out.float(), ref.float(), atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.gpu
+def test_integration_decode_binding_matches_oracle(cuda):
+    decode_via_c_abi = _integration_binding("decode_via_c_abi")
+    lens_k = [300, 5000, 1234, 1, 70]
+    case = testing.make_case("ctypes_decode", [1] * 5, lens_k, 8, 2, 128, torch.bfloat16,
+                             seed=54, causal=False)
+    c = case.to(cuda)
+    print("ctypes decode binding: 5 caches", flush=True)
+    out, lse = decode_via_c_abi(c.q, c.k, c.v, c.rel, c.cu_q, c.cu_k, c.max_k, c.rel_extent,
+                                scale=c.scale)
+    torch.cuda.synchronize()
+    want_out, want_lse = ref_rel_attn_with_lse(case.q, case.k, case.v, case.rel, case.cu_q,
+                                               case.cu_k, case.scale, case.rel_extent,
+                                               causal=False)
+    torch.testing.assert_close(out.cpu().float(), want_out.float(), atol=ATOL, rtol=RTOL)
+    torch.testing.assert_close(lse.cpu(), want_lse, atol=LSE_ATOL, rtol=0)
 
 
 @pytest.mark.gpu
