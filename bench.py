@@ -235,6 +235,29 @@ def per_token_bias_bench(steps, warmup, rel_extent, seq_len=4096, batch=8):
             "rel_bytes": case.rel.numel() * case.rel.element_size()}
 
 
+def decode_small_bench(steps, warmup, shapes=((1, 8192), (1, 32768), (1, 131072), (4, 8192))):
+    """Decode at serving batch sizes: `batch` sequences of `keys` cached keys each
+    (Hq 8 / Hkv 2, d 128, bf16, non-causal: every key streamed); us per call and
+    the KV rate."""
+    import torch
+    from inkling_fa4 import inkling_fa4_rel_attention_decode, testing
+
+    rows = {}
+    for batch, keys in shapes:
+        case = testing.make_case("decode_small", [1] * batch, [keys] * batch, 8, 2, 128,
+                                 torch.bfloat16, seed=23, causal=False)
+        c = case.to("cuda")
+        args = c.args()
+        ms = time_gpu(lambda: inkling_fa4_rel_attention_decode(*args, causal=False), steps,
+                      warmup)
+        kv_bytes = batch * keys * 2 * 128 * 2 * 2
+        rows[f"{batch}x{keys}"] = {"us": round(ms * 1e3, 2),
+                                   "gbps": round(kv_bytes / (ms * 1e-3) / 1e9, 1)}
+        log(f"decode {batch} x {keys} keys: {ms * 1e3:.1f} us")
+        del c, args
+    return rows
+
+
 def decode_bench(steps, warmup, block_size=0, fp8=False):
     """Decode over the 64-sequence batch; block_size > 0: the same keys in a
     paged cache of that block size (blocks in a shuffled physical order);
@@ -505,6 +528,7 @@ def main():
         log(f"decode fp8: {d8['us']:.1f} us  {d8['gbps']:.0f} GB/s")
         result["decode_fp8"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                 for k, v in d8.items()}
+        result["decode_small_batch"] = decode_small_bench(args.steps, args.warmup)
         if result["value"] is None:
             result["value"] = round(dec["gbps"], 1)
             result["unit"] = "GB/s"

@@ -600,24 +600,30 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   }
 }
 
-constexpr int kCombineWaves = 4;
+constexpr int kCombineWaves = 8;
 
 // One workgroup per (head, sequence).  Two dependent memory rounds: the
 // sequence bounds and the segment's wave range (independent loads), then the
-// parts themselves.  Wave v merges parts v, v+4, ... online (running max,
-// rescaled sums, loads of later parts in flight); the four wave results meet in
-// LDS.
+// parts themselves.  Thread (g, c) holds 16-byte chunk c of the head's row and
+// merges parts g, g + kGroups, ... online (running max, rescaled sums, four
+// parts' loads in flight); the kGroups results of a chunk meet in LDS.  With
+// D / 4 chunks per row and 8 waves that is 16 groups at D = 128 (32 at
+// D = 64), so a segment of up to 64 (128) parts merges in one round of loads;
+// a few long caches spread over many waves (one sequence of 128K keys over
+// 896 waves: ~450 parts per cache) take a handful of rounds.
 template <int D, typename Tag>
 __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(DecodeParams p) {
   using E = Elem<Tag>;
-  constexpr int kPer = D / 64;  // d values per lane
-  __shared__ float part_o[kCombineWaves][64 * kPer];
-  __shared__ float part_m[kCombineWaves];
-  __shared__ float part_l[kCombineWaves];
+  constexpr int kThreads = 64 * kCombineWaves;
+  constexpr int kChunks = D / 4;                // 16-byte chunks of a row
+  constexpr int kGroups = kThreads / kChunks;   // part groups
+  __shared__ f32x4_t part_o[kGroups][kChunks];
+  __shared__ float part_m[kGroups];
+  __shared__ float part_l[kGroups];
   const int head = blockIdx.x;
   const int seq = blockIdx.y;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
+  const int c = tid % kChunks, grp = tid / kChunks;
   const int ga = p.group;
   const int kvh = head / ga, h = head % ga;
   const int seg = seq * p.kv_heads + kvh;
@@ -629,15 +635,11 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
   if (lq != 1) {
     // Not one query token (cu_seqlens_q is not arange): the pass above streamed
     // nothing for this sequence; its query rows, if any, get out = 0, lse = -inf.
-    for (int row = wave; row < lq; row += kCombineWaves) {
+    for (int row = grp; row < lq; row += kGroups) {
       uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)(qs + row) * p.o_st +
-                      (int64_t)head * p.o_sh + kPer * lane;
-      if constexpr (kPer == 2) {
-        *reinterpret_cast<uint32_t*>(dst) = 0u;
-      } else {
-        *dst = 0;
-      }
-      if (p.lse != nullptr && lane == 0) p.lse[(int64_t)head * p.lse_sh + qs + row] = -INFINITY;
+                      (int64_t)head * p.o_sh + 4 * c;
+      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{0u, 0u};
+      if (p.lse != nullptr && c == 0) p.lse[(int64_t)head * p.lse_sh + qs + row] = -INFINITY;
     }
     return;
   }
@@ -649,61 +651,47 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
   }
   // part i of the segment lives in slot seg + w_first + i
   const float* lse_s = p.ws_lse + (int64_t)(seg + w_first) * ga + h;
-  const float* o_s = p.ws_o + ((int64_t)(seg + w_first) * ga + h) * D + kPer * lane;
+  const float* o_s = p.ws_o + ((int64_t)(seg + w_first) * ga + h) * D + 4 * c;
   const int64_t o_stride = (int64_t)ga * D;
 
   float m = -INFINITY, l = 0.f;
-  float acc[kPer];
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) acc[e] = 0.f;
+  f32x4_t acc{};
 #pragma unroll 4
-  for (int s = wave; s < parts; s += kCombineWaves) {
+  for (int s = grp; s < parts; s += kGroups) {
     const float ls = lse_s[(int64_t)s * ga];
-    float os[kPer];
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) os[e] = o_s[s * o_stride + e];
+    const f32x4_t os = *reinterpret_cast<const f32x4_t*>(o_s + s * o_stride);
     const float mn = fmaxf(m, ls);
     const float mu = mn == -INFINITY ? 0.f : mn;
     const float a_old = fast_exp2(m - mu), a_new = fast_exp2(ls - mu);
     l = l * a_old + a_new;
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) acc[e] = acc[e] * a_old + a_new * os[e];
+    acc = acc * a_old + a_new * os;
     m = mn;
   }
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) part_o[wave][kPer * lane + e] = acc[e];
-  if (lane == 0) {
-    part_m[wave] = m;
-    part_l[wave] = l;
+  part_o[grp][c] = acc;
+  if (c == 0) {  // every thread of a group has merged the same parts: one m, l
+    part_m[grp] = m;
+    part_l[grp] = l;
   }
   __syncthreads();
-  if (wave != 0) return;
+  if (grp != 0) return;
   float mt = part_m[0];
 #pragma unroll
-  for (int v = 1; v < kCombineWaves; ++v) mt = fmaxf(mt, part_m[v]);
+  for (int g = 1; g < kGroups; ++g) mt = fmaxf(mt, part_m[g]);
   const float mu = mt == -INFINITY ? 0.f : mt;
   float lt = 0.f;
-  float out[kPer];
+  f32x4_t out{};
 #pragma unroll
-  for (int e = 0; e < kPer; ++e) out[e] = 0.f;
-#pragma unroll
-  for (int v = 0; v < kCombineWaves; ++v) {
-    const float a = fast_exp2(part_m[v] - mu);
-    lt += a * part_l[v];
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) out[e] += a * part_o[v][kPer * lane + e];
+  for (int g = 0; g < kGroups; ++g) {
+    const float a = fast_exp2(part_m[g] - mu);
+    lt += a * part_l[g];
+    out += a * part_o[g][c];
   }
-
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)qs * p.o_st + (int64_t)head * p.o_sh +
-                  kPer * lane;
-  if constexpr (kPer == 2) {
-    *reinterpret_cast<uint32_t*>(dst) = E::pack2(out[0] * inv, out[1] * inv);
-  } else {
-    const uint32_t wv = E::pack2(out[0] * inv, 0.f);
-    *dst = (uint16_t)(wv & 0xffffu);
-  }
-  if (p.lse != nullptr && lane == 0) {
+                  4 * c;
+  *reinterpret_cast<u32x2_t*>(dst) =
+      u32x2_t{E::pack2(out[0] * inv, out[1] * inv), E::pack2(out[2] * inv, out[3] * inv)};
+  if (p.lse != nullptr && c == 0) {
     p.lse[(int64_t)head * p.lse_sh + qs] = lt > 0.f ? (mu + __log2f(lt)) * kLn2 : -INFINITY;
   }
 }

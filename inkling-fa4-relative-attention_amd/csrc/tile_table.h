@@ -71,13 +71,40 @@ inline int64_t decode_max_steps(int64_t batch, int64_t kv_heads, int64_t max_seq
   return batch * kv_heads * ((keys + kDecodeStep - 1) / kDecodeStep);
 }
 
+// Small calls (few caches, or few steps): at least kDecodeMinSteps 32-key
+// steps per wave, and at most kDecodeMaxParts waves per (sequence, kv head)
+// cache -- or, for caches longer than kDecodeMaxParts * kDecodePartSteps
+// steps, one wave per kDecodePartSteps steps -- so that the combine's merge
+// stays a few rounds of loads while long caches keep enough waves streaming.
+// Same-session sweeps, Hq 8 / Hkv 2, d 128, bf16, non-causal
+// (profiles/sweep_decode_small.md).
+#ifndef IFA4_DECODE_MIN_STEPS
+#define IFA4_DECODE_MIN_STEPS 2
+#endif
+#ifndef IFA4_DECODE_MAX_PARTS
+#define IFA4_DECODE_MAX_PARTS 128
+#endif
+#ifndef IFA4_DECODE_PART_STEPS
+#define IFA4_DECODE_PART_STEPS 8
+#endif
+constexpr int64_t kDecodeMinSteps = IFA4_DECODE_MIN_STEPS;
+constexpr int64_t kDecodeMaxParts = IFA4_DECODE_MAX_PARTS;
+constexpr int64_t kDecodePartSteps = IFA4_DECODE_PART_STEPS;
+
 inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seqlen_k,
                                 bool key0_only, bool fp8, bool paged) {
   const int64_t t = decode_max_steps(batch, kv_heads, max_seqlen_k, key0_only);
   int64_t w = kDecodeWaves;
   if (paged && kDecodeWavesPaged > w) w = kDecodeWavesPaged;
   if (fp8 && kDecodeWavesFp8 > w) w = kDecodeWavesFp8;
-  return (int32_t)(t < w ? t : w);
+  const int64_t by_steps = (t + kDecodeMinSteps - 1) / kDecodeMinSteps;
+  const int64_t seg_steps = batch * kv_heads > 0 ? t / (batch * kv_heads) : 0;
+  const int64_t long_parts = (seg_steps + kDecodePartSteps - 1) / kDecodePartSteps;
+  const int64_t by_parts =
+      batch * kv_heads * (long_parts > kDecodeMaxParts ? long_parts : kDecodeMaxParts);
+  if (by_steps < w) w = by_steps;
+  if (by_parts < w) w = by_parts;
+  return (int32_t)w;
 }
 
 // Split KV for prefill calls whose grid leaves the chip underfilled (few

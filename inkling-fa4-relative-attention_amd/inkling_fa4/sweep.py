@@ -45,6 +45,8 @@ Knobs (macros of the kernel sources):
                                               batch of a tile's DMAs (0)
   decode_fwd.hip   IFA4_DECODE_WPE            waves per SIMD the stream pass's registers target
   tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
+                   IFA4_DECODE_MIN_STEPS      fewest 32-key steps per wave (small calls)
+                   IFA4_DECODE_MAX_PARTS      most waves per (sequence, kv head) cache
                    IFA4_DECODE_WAVES_FP8      the same for an fp8 KV cache (workload decode_fp8)
                    IFA4_DECODE_WAVES_PAGED    the same for a paged cache (workload decode_paged)
                    IFA4_PREFILL_SPLIT_MAX_GRID  largest prefill grid the table splits (split KV)
@@ -150,6 +152,13 @@ def _case(workload, seq, batch=1, heads=4):
             name, lens, lens, 8, 2, 128, torch.bfloat16, seed=seed, rel_extent=ext,
             rel_table=False, rel_dtype=rd)
         return mk("sweep_check", [1300, 64, 33], 2), mk("per_token", [seq] * 8, 3)
+    if workload == "decode_small":
+        # --batch sequences of --seq cached keys each (serving at small batch)
+        lens = [seq] * batch
+        return (testing.make_case("sweep_check", [1] * 3, [300, 5000, 77], 8, 2, 128,
+                                  torch.bfloat16, seed=21, causal=False),
+                testing.make_case("decode_small", [1] * batch, lens, 8, 2, 128,
+                                  torch.bfloat16, seed=22, causal=False))
     return testing.decode(batch=8, seed=21, causal=False), testing.decode(causal=False)
 
 
@@ -382,11 +391,11 @@ def main(argv=None):
         r.add_argument("--workload", choices=["prefill", "prefill_reference", "prefill_token",
                                               "prefill_token1024",
                                               "rproj128", "rproj512", "rproj1024", "decode",
-                                              "decode_fp8", "decode_paged"],
+                                              "decode_small", "decode_fp8", "decode_paged"],
                        default="prefill")
         r.add_argument("--seq", type=int, default=4096)
         r.add_argument("--batch", type=int, default=1,
-                       help="prefill_reference: sequences of --seq tokens")
+                       help="prefill_reference / decode_small: sequences of --seq tokens")
         r.add_argument("--heads", type=int, default=4, help="prefill_reference: Hq = Hkv")
         r.add_argument("--steps", type=int, default=30)
         r.add_argument("--warmup", type=int, default=5)

@@ -31,6 +31,9 @@ ATOL, RTOL, LSE_ATOL = 2e-2, 2e-2, 1e-3
 STEP = 32
 RESCALE_LOG2 = 8.0
 WAVE_COUNTS = (896, 2048)  # contiguous 16-bit; paged or fp8 (the tile table)
+# the table's small-call caps: steps per wave; waves per cache (or one per
+# PART_STEPS steps of a longer cache)
+MIN_STEPS, MAX_PARTS, PART_STEPS = 2, 128, 8
 LENS_K = [30000, 1, 7000, 16384, 33, 12000, 64, 20000, 9001, 5000, 31000, 2500]
 
 
@@ -71,10 +74,15 @@ def _step_maxima(case):
 def _rescale_waves(maxima, waves, max_k, batch, hkv):
     """(P, number of waves whose range raises one head's max by more than the
     threshold after the wave's first step of a cache) for a stream of `waves`
-    persistent waves (capped at the step bound of the call, as the library does)."""
+    persistent waves, capped as the library caps them: at least MIN_STEPS steps
+    of the call's step bound per wave, at most max(MAX_PARTS, steps of the
+    longest cache / PART_STEPS) waves per cache."""
     seg_steps = [m.shape[0] for m in maxima]
     total = sum(seg_steps)
-    w = min(waves, batch * hkv * ((max_k + STEP - 1) // STEP))
+    per_seg = (max_k + STEP - 1) // STEP
+    bound = batch * hkv * per_seg
+    w = min(waves, -(-bound // MIN_STEPS),
+            batch * hkv * max(MAX_PARTS, -(-per_seg // PART_STEPS)))
     p = (total + w - 1) // w
     starts, acc = [], 0
     for n in seg_steps:
