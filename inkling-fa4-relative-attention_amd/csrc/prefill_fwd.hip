@@ -384,9 +384,8 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
 #if IFA4_DMA2
   // Each wave DMAs rows of one tensor (K for the first half of the waves, V for
   // the second).  A lane's offset within a DMA depends on the tile only through
-  // kb (added as the scalar offset) and on the block only through the swizzle
-  // of its tile row and a row shift (also scalar): one register per DMA of the
-  // wave, set once.
+  // kb (the scalar offset, one multiply per tile): one register per DMA of the
+  // wave (its tile row's offset and swizzled chunk), set once.
   static_assert(St::kDmaPerWave <= St::kDmaPerTensor && St::kDmaPerTensor % St::kDmaPerWave == 0,
                 "a wave's DMAs stay within one tensor");
   const bool dma_v = wave * St::kDmaPerWave >= St::kDmaPerTensor;
@@ -398,18 +397,18 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
     const int id = wave * St::kDmaPerWave + u;
     const int blk = dma_v ? id - St::kDmaPerTensor : id;
     const int row = blk * St::kRowsPerDma + dma_row;  // tile row
-    dma_voff[u] = (uint32_t)dma_row * dma_rowb + 16u * (uint32_t)(dma_slot ^ swz<St::kChunks>(row));
+    dma_voff[u] = (uint32_t)row * dma_rowb + 16u * (uint32_t)(dma_slot ^ swz<St::kChunks>(row));
   }
   const uint32_t lds_stages = lds_addr(stages);
   auto dma_tile = [&](int kt, uint16_t* stage) {
     const int kb = kt * kBlockK;
     const uint32_t stage_lds = lds_stages + (uint32_t)((stage - stages) * 2);
     if (!IFA4_DMA_COVER_EACH) hazard_nop5();  // batch cover (sweep knob)
+    const uint32_t soff = (uint32_t)kb * dma_rowb;  // the tile's first row
 #pragma unroll
     for (int u = 0; u < St::kDmaPerWave; ++u) {
       const int id = wave * St::kDmaPerWave + u;
       const int blk = dma_v ? id - St::kDmaPerTensor : id;
-      const uint32_t soff = (uint32_t)(kb + blk * St::kRowsPerDma) * dma_rowb;
       const uint32_t dst = stage_lds + (uint32_t)(((dma_v ? St::kTile : 0) + blk * 512) * 2);
       dma_16_so(dma_r, dma_voff[u], soff, dst);
     }
