@@ -528,7 +528,8 @@ def main():
         log(f"decode fp8: {d8['us']:.1f} us  {d8['gbps']:.0f} GB/s")
         result["decode_fp8"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                 for k, v in d8.items()}
-        result["decode_small_batch"] = decode_small_bench(args.steps, args.warmup)
+        if not args.no_sweep:  # (kept out of profiling runs: same kernel, other shapes)
+            result["decode_small_batch"] = decode_small_bench(args.steps, args.warmup)
         if result["value"] is None:
             result["value"] = round(dec["gbps"], 1)
             result["unit"] = "GB/s"
