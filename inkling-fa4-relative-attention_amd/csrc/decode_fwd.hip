@@ -20,23 +20,24 @@
 // split needs no host synchronisation and no atomics.
 //
 // Pass 1 (decode_stream_kernel), per 32-key step of a segment:
-//   * K and V rows arrive with coalesced, non-temporal 16-byte buffer loads one
-//     step ahead of the compute (register double buffering), rows past the
-//     segment end read as zero; the next segment's Q (all G query heads of the kv head)
-//     arrives ahead of it by LDS DMA into a two-slot ring;
+//   * K and V rows arrive with coalesced, non-temporal 16-byte buffer loads
+//     kNbuf - 1 steps ahead of the compute (a ring of register buffers), rows
+//     past the segment end read as zero; the next segment's Q (all G query
+//     heads of the kv head) arrives ahead of it by LDS DMA into a ring of kNbuf
+//     slots;
 //   * K goes through a small padded LDS tile into the A operand of
 //     S^T = K Q^T on v_mfma_f32_16x16x32 (B = the G query rows, zero padded to
-//     16 columns);
+//     16 columns); an fp8 cache converts to the 16-bit type on the way;
 //   * online softmax per head (exp2, deferred rescale);
-//   * O += P V on the VALU: a lane holds one 16-byte chunk of a V row and reads
-//     that key's G probabilities from LDS (broadcast).
+//   * O^T += V^T P^T on v_mfma_f32_16x16x32: V through a swizzled LDS tile read
+//     with transposing ds_read_b64_tr_b16, P^T straight from the S^T layout.
 // Partial of (segment s, wave w) -> workspace slot s + w (slots increase with
 // w, so the map is one-to-one); the wave holding a segment's first step also
 // records the range of waves that cover the segment.
 //
 // Pass 2 (decode_combine_kernel): per (head, sequence) merge of the segment's
-// partials by log-sum-exp (four waves share them, each merging online); writes
-// out (q dtype) and lse (natural log).
+// partials by log-sum-exp (16 part groups of a workgroup each merge online,
+// then meet in LDS); writes out (q dtype) and lse (natural log).
 #include "ifa4_device.hpp"
 #include "ifa4_kernels.h"
 

@@ -9,7 +9,8 @@
 // (sequence, head).  Each wave owns NQB blocks of 32 rows.  K/V tiles of
 // BLOCK_K = 64 keys go from HBM straight into LDS with buffer_load ... lds
 // (no registers, no LDS store instructions); two LDS stages, the DMA of the
-// next tile is in flight while the current one is computed.  Two shapes:
+// next tile is in flight while the current one is computed.  Two shapes (the
+// library builds NQB = 1; NQB = 2 is the sweep knob IFA4_PREFILL_NQB):
 //   NQB = 2: 2 waves x 64 rows, 1 wave per SIMD with up to 512 registers;
 //            every K / V^T fragment read from LDS feeds two MFMAs, and the two
 //            independent row blocks let one block's softmax overlap the other
@@ -27,9 +28,10 @@
 // lane) is two ds_read_b64_tr_b16 transposing reads: within a 16-lane group,
 // source lane j pointing at V[k0 + j/4][d0 + 4(j%4)] returns to lane i the
 // four values V[k0 .. k0+3][d0 + i], which is exactly the key order of P.
-// LDS rows are stored with their 16-byte chunks XOR-swizzled by
-// f(row) = 4(row & 3) | ((row >> 2) & 3), so the 8-row K reads and the
-// 4-row transposing V reads each hit distinct banks.
+// LDS rows are stored with their 16-byte chunks XOR-swizzled (swz below: at
+// d 128, f(row) = 4(row & 3) | ((row >> 2) & 1) | 2((row >> 4) & 1)), so the K
+// reads (rows {0..7, 16..23} or {8..15, 24..31} of a 32-key block per pass)
+// and the 4-row transposing V reads each hit distinct banks.
 //
 // Memory access.  Q/K/V rows and bias values are read with buffer loads over
 // per-(sequence, head) resources: rows past the sequence end fall outside the
