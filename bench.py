@@ -135,8 +135,9 @@ def prefill_bias_variants(steps, warmup, seq_len=4096, batch=8):
     fp32 (what the reference operator takes) and from the fused RelLogitsProj
     factors r [Tq, Hq, 16], W [16, R'] (no rel_logits in HBM): R' = 128 with
     fp32 r, and the serving model's global extent 1024 with fp32 and bf16 r,
-    next to the einsum that would materialise its [Tq, Hq, 1024] bf16
-    rel_logits for the per-token path."""
+    next to the products that would materialise the per-token path's
+    rel_logits from the same factors: [Tq, Hq, 128] fp32 and [Tq, Hq, 1024]
+    bf16 (the per-token path's end-to-end time is that plus the attention)."""
     import torch
     from inkling_fa4 import (inkling_fa4_rel_attention, inkling_fa4_rel_attention_rproj,
                              testing)
@@ -158,6 +159,9 @@ def prefill_bias_variants(steps, warmup, seq_len=4096, batch=8):
             res[key] = time_gpu(lambda: inkling_fa4_rel_attention_rproj(
                 c.q, c.k, c.v, r_in, w, c.cu_q, c.cu_k, c.max_q, c.max_k, ext, causal=True,
                 softmax_scale=c.scale), steps, warmup)
+        if ext == 128:  # fp32 [Tq * Hq, 16] @ [16, 128], as the per-token leg reads it
+            res["materialise_rel128_ms"] = time_gpu(
+                lambda: torch.matmul(r.view(-1, 16), w), steps, warmup)
         if ext == 1024:
             res["materialise_rel1024_ms"] = time_gpu(
                 lambda: torch.einsum("thc,cd->thd", r, w).to(torch.bfloat16), steps, warmup)
@@ -493,7 +497,8 @@ def main():
                                  "frac_of_peak": round(r["frac_of_peak"], 4)}
             result["prefill_sweep"] = sweep
             bv = prefill_bias_variants(max(5, args.steps // 2), max(2, args.warmup // 2), args.seq)
-            log(f"prefill seq {args.seq}, per-token bias: {bv['per_token_rel_ms']:.4f} ms; "
+            log(f"prefill seq {args.seq}, per-token bias: {bv['per_token_rel_ms']:.4f} ms "
+                f"(+ {bv['materialise_rel128_ms']:.4f} ms to materialise it); "
                 f"fused RelLogitsProj: {bv['rproj_ms']:.4f} ms; at rel_extent 1024: "
                 f"{bv['rproj_rel1024_ms']:.4f} ms (bf16 r {bv['rproj_rel1024_bf16r_ms']:.4f}), "
                 f"materialising its rel_logits: {bv['materialise_rel1024_ms']:.4f} ms")
