@@ -47,6 +47,11 @@
 #ifndef IFA4_FP8_CVT2
 #define IFA4_FP8_CVT2 1
 #endif
+// Split the combine of segments with many parts over several workgroups
+// (sweep knob; 0: one workgroup per (head, sequence)).
+#ifndef IFA4_COMBINE_SPLIT
+#define IFA4_COMBINE_SPLIT 1
+#endif
 // Register budget of the stream pass: at least this many waves per SIMD
 // (2: at most 256 VGPRs, so that 2048 persistent waves fit in one round).
 #ifndef IFA4_DECODE_WPE
@@ -603,28 +608,34 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
 
 constexpr int kCombineWaves = 8;
 
-// One workgroup per (head, sequence).  Two dependent memory rounds: the
+// SPLIT workgroups per (head, sequence), workgroup z over the 16-byte chunks
+// [z, z + 1) * D / (4 SPLIT) of the row.  Two dependent memory rounds: the
 // sequence bounds and the segment's wave range (independent loads), then the
-// parts themselves.  Thread (g, c) holds 16-byte chunk c of the head's row and
-// merges parts g, g + kGroups, ... online (running max, rescaled sums, four
-// parts' loads in flight); the kGroups results of a chunk meet in LDS.  With
-// D / 4 chunks per row and 8 waves that is 16 groups at D = 128 (32 at
-// D = 64), so a segment of up to 64 (128) parts merges in one round of loads;
-// a few long caches spread over many waves (one sequence of 128K keys over
-// 896 waves: ~450 parts per cache) take a handful of rounds.
-template <int D, typename Tag>
+// parts themselves.  Thread (g, c) holds chunk c and merges parts g, g +
+// kGroups, ... online (running max, rescaled sums, four parts' loads in
+// flight); the kGroups results of a chunk meet in LDS.  With 8 waves that is
+// 16 groups per split at D = 128 (32 at D = 64), so a segment of up to 64
+// (128) parts per split merges in one round of loads.  The host takes more
+// splits for segments of many parts (a few long caches spread over many
+// waves: one sequence of 128K keys over 1024 waves has ~512 parts per cache).
+// Every split merges the same parts in the same order, so the running max and
+// sum, and with them the normalisation, are the same bits in all of them; split
+// 0 writes the LSE.
+template <int D, typename Tag, int SPLIT>
 __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(DecodeParams p) {
   using E = Elem<Tag>;
   constexpr int kThreads = 64 * kCombineWaves;
-  constexpr int kChunks = D / 4;                // 16-byte chunks of a row
+  constexpr int kChunks = D / 4 / SPLIT;        // 16-byte chunks of this split
   constexpr int kGroups = kThreads / kChunks;   // part groups
   __shared__ f32x4_t part_o[kGroups][kChunks];
   __shared__ float part_m[kGroups];
   __shared__ float part_l[kGroups];
   const int head = blockIdx.x;
   const int seq = blockIdx.y;
+  const int split = blockIdx.z;
   const int tid = threadIdx.x;
   const int c = tid % kChunks, grp = tid / kChunks;
+  const int cc = split * kChunks + c;  // chunk of the row
   const int ga = p.group;
   const int kvh = head / ga, h = head % ga;
   const int seg = seq * p.kv_heads + kvh;
@@ -638,9 +649,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
     // nothing for this sequence; its query rows, if any, get out = 0, lse = -inf.
     for (int row = grp; row < lq; row += kGroups) {
       uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)(qs + row) * p.o_st +
-                      (int64_t)head * p.o_sh + 4 * c;
+                      (int64_t)head * p.o_sh + 4 * cc;
       *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{0u, 0u};
-      if (p.lse != nullptr && c == 0) p.lse[(int64_t)head * p.lse_sh + qs + row] = -INFINITY;
+      if (p.lse != nullptr && cc == 0) p.lse[(int64_t)head * p.lse_sh + qs + row] = -INFINITY;
     }
     return;
   }
@@ -652,7 +663,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
   }
   // part i of the segment lives in slot seg + w_first + i
   const float* lse_s = p.ws_lse + (int64_t)(seg + w_first) * ga + h;
-  const float* o_s = p.ws_o + ((int64_t)(seg + w_first) * ga + h) * D + 4 * c;
+  const float* o_s = p.ws_o + ((int64_t)(seg + w_first) * ga + h) * D + 4 * cc;
   const int64_t o_stride = (int64_t)ga * D;
 
   float m = -INFINITY, l = 0.f;
@@ -689,10 +700,10 @@ __global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(Deco
   }
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)qs * p.o_st + (int64_t)head * p.o_sh +
-                  4 * c;
+                  4 * cc;
   *reinterpret_cast<u32x2_t*>(dst) =
       u32x2_t{E::pack2(out[0] * inv, out[1] * inv), E::pack2(out[2] * inv, out[3] * inv)};
-  if (p.lse != nullptr && c == 0) {
+  if (p.lse != nullptr && cc == 0) {
     p.lse[(int64_t)head * p.lse_sh + qs] = lt > 0.f ? (mu + __log2f(lt)) * kLn2 : -INFINITY;
   }
 }
@@ -715,8 +726,22 @@ hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((decode_combine_kernel<D, Tag>), dim3(p.n_heads, p.batch),
-                     dim3(64 * kCombineWaves), 0, stream, p);
+  // Splits of the combine: enough part groups that the parts of a segment
+  // (about waves / segments + 1 when the caches are of similar length) merge in
+  // one round of four loads per thread, at most 4.
+  const int64_t segs = (int64_t)p.batch * p.kv_heads;
+  const int64_t parts = segs > 0 ? (int64_t)p.n_waves / segs + 1 : 1;
+  constexpr int64_t kRound = 4 * (64 * kCombineWaves) / (D / 4);  // parts per round, 1 split
+  const dim3 block(64 * kCombineWaves);
+  if (IFA4_COMBINE_SPLIT && parts > 2 * kRound)
+    hipLaunchKernelGGL((decode_combine_kernel<D, Tag, 4>), dim3(p.n_heads, p.batch, 4), block, 0,
+                       stream, p);
+  else if (IFA4_COMBINE_SPLIT && parts > kRound)
+    hipLaunchKernelGGL((decode_combine_kernel<D, Tag, 2>), dim3(p.n_heads, p.batch, 2), block, 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((decode_combine_kernel<D, Tag, 1>), dim3(p.n_heads, p.batch), block, 0,
+                       stream, p);
   return hipGetLastError();
 }
 

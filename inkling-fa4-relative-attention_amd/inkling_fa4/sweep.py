@@ -44,6 +44,8 @@ Knobs (macros of the kernel sources):
   ifa4_device.hpp  IFA4_DMA_COVER_EACH        hazard cover on every LDS DMA (1) or one per
                                               batch of a tile's DMAs (0)
   decode_fwd.hip   IFA4_DECODE_WPE            waves per SIMD the stream pass's registers target
+                   IFA4_COMBINE_SPLIT         combine of many-part segments over 2 or 4
+                                              workgroups per (head, sequence) (0/1)
   tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
                    IFA4_DECODE_MIN_STEPS      fewest 32-key steps per wave (small calls)
                    IFA4_DECODE_MAX_PARTS      most waves per (sequence, kv head) cache

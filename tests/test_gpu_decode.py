@@ -123,8 +123,10 @@ def test_decode_stream_many_short_caches(cuda, causal):
 
 
 def test_decode_stream_one_cache_over_all_waves(cuda):
-    """One 70,000-key cache per kv head: 2,188 steps each, 2,048 waves, so every
-    wave holds a piece and the merge of a head sums ~1,000 partials."""
+    """One 70,000-key cache per kv head: 2,188 steps each over 548 waves (the
+    small-call cap, max(128, steps / 8) waves per cache), so every wave holds a
+    piece and the merge of a head sums ~275 partials (four combine workgroups
+    per head, each over a quarter of the row)."""
     case = testing.make_case("dec_long", [1], [70000], 8, 2, 128, torch.bfloat16, seed=13,
                              causal=False)
     _check(_decode(case, cuda), _oracle(case))
@@ -137,4 +139,18 @@ def test_decode_stream_step_boundaries(cuda, head_dim):
     lens = [31, 32, 33, 63, 64, 65, 95, 96, 97, 4096, 4097, 4127, 4128, 4129] * 5
     case = testing.make_case("dec_steps", [1] * len(lens), lens, 4, 4, head_dim, torch.bfloat16,
                              seed=14, causal=False)
+    _check(_decode(case, cuda), _oracle(case))
+
+
+@pytest.mark.parametrize("keys,head_dim", [(8192, 64), (8192, 128), (131072, 64), (131072, 128)])
+def test_decode_one_sequence_split_combine(cuda, keys, head_dim):
+    """One sequence spread over many waves: ~129 partials per (head, sequence)
+    at 8K keys (256 waves), ~449 at 128K (896 waves).  The combine then splits
+    each row's 16-byte chunks over 2 workgroups (8K keys, d 64) or 4 (the
+    rest), each merging every partial for its slice; all splits must agree on
+    the normalisation, and split 0 writes the LSE.  Reference semantics:
+    src/inkling_fa4/reference.py:38-39."""
+    case = testing.make_case("dec_split", [1], [keys], 8, 2, head_dim, torch.bfloat16,
+                             seed=15, causal=False)
+    print(f"one sequence of {keys} keys, d {head_dim}", flush=True)
     _check(_decode(case, cuda), _oracle(case))
