@@ -74,10 +74,13 @@ inline int64_t decode_max_steps(int64_t batch, int64_t kv_heads, int64_t max_seq
 // Small calls (few caches, or few steps): at least kDecodeMinSteps 32-key
 // steps per wave, and at most kDecodeMaxParts waves per (sequence, kv head)
 // cache -- or, for caches longer than kDecodeMaxParts * kDecodePartSteps
-// steps, one wave per kDecodePartSteps steps -- so that the combine's merge
-// stays a few rounds of loads while long caches keep enough waves streaming.
-// Same-session sweeps, Hq 8 / Hkv 2, d 128, bf16, non-causal
-// (profiles/sweep_decode_small.md).
+// steps, one wave per kDecodePartSteps steps.  With the combine split over
+// several workgroups for many-part segments, a part of 2 steps (the same as the
+// floor per wave, which then is the binding cap) measured fastest: one
+// sequence of 16K / 32K / 64K keys 14.8 / 21.2 / 23.6 -> 12.9 / 15.8 / 21.3 us
+// (8 steps per part before), fp8 cache 32K 21.9 -> 15.0, paged 32K 30.0 -> 18.6;
+// 8K, 128K and the 64-sequence batch unchanged.  Same-session sweeps, Hq 8 /
+// Hkv 2, d 128, non-causal (profiles/sweep_decode_small.md).
 #ifndef IFA4_DECODE_MIN_STEPS
 #define IFA4_DECODE_MIN_STEPS 2
 #endif
@@ -85,7 +88,7 @@ inline int64_t decode_max_steps(int64_t batch, int64_t kv_heads, int64_t max_seq
 #define IFA4_DECODE_MAX_PARTS 128
 #endif
 #ifndef IFA4_DECODE_PART_STEPS
-#define IFA4_DECODE_PART_STEPS 8
+#define IFA4_DECODE_PART_STEPS 2
 #endif
 constexpr int64_t kDecodeMinSteps = IFA4_DECODE_MIN_STEPS;
 constexpr int64_t kDecodeMaxParts = IFA4_DECODE_MAX_PARTS;

@@ -154,8 +154,9 @@ def _case(workload, seq, batch=1, heads=4):
             name, lens, lens, 8, 2, 128, torch.bfloat16, seed=seed, rel_extent=ext,
             rel_table=False, rel_dtype=rd)
         return mk("sweep_check", [1300, 64, 33], 2), mk("per_token", [seq] * 8, 3)
-    if workload == "decode_small":
-        # --batch sequences of --seq cached keys each (serving at small batch)
+    if workload.startswith("decode_small"):
+        # --batch sequences of --seq cached keys each (serving at small batch);
+        # _fp8 / _paged: the same keys as an fp8 or a paged cache
         lens = [seq] * batch
         return (testing.make_case("sweep_check", [1] * 3, [300, 5000, 77], 8, 2, 128,
                                   torch.bfloat16, seed=21, causal=False),
@@ -183,14 +184,14 @@ def _call(workload, case, return_lse):
           else inkling_fa4_rel_attention_decode)
     args = case.args()
     kw = {}
-    if workload == "decode_paged":  # the same keys in blocks of 16, shuffled
+    if workload in ("decode_paged", "decode_small_paged"):  # blocks of 16, shuffled
         pk = testing.paginate(case.to("cpu"), block_size=16, seed=0, spare_blocks=0,
                               fill=0.0).to(case.q.device)
         return lambda: inkling_fa4_rel_attention_decode_paged(
             case.q, pk.k_cache, pk.v_cache, case.rel, case.cu_q, pk.seqused_k, pk.block_table,
             case.max_q, case.max_k, case.rel_extent, causal=case.causal,
             window_size=case.window_size, softmax_scale=case.scale, return_lse=return_lse)
-    if workload == "decode_fp8":  # the same keys as an fp8 cache, per-tensor scales
+    if workload in ("decode_fp8", "decode_small_fp8"):  # fp8 cache, per-tensor scales
         k8, v8, ks, vs, _ = testing.fp8_kv(case)
         args = (args[0], k8, v8) + args[3:]
         kw = {"k_scale": ks, "v_scale": vs}
@@ -393,11 +394,13 @@ def main(argv=None):
         r.add_argument("--workload", choices=["prefill", "prefill_reference", "prefill_token",
                                               "prefill_token1024",
                                               "rproj128", "rproj512", "rproj1024", "decode",
-                                              "decode_small", "decode_fp8", "decode_paged"],
+                                              "decode_small", "decode_small_fp8",
+                                              "decode_small_paged", "decode_fp8",
+                                              "decode_paged"],
                        default="prefill")
         r.add_argument("--seq", type=int, default=4096)
         r.add_argument("--batch", type=int, default=1,
-                       help="prefill_reference / decode_small: sequences of --seq tokens")
+                       help="prefill_reference / decode_small*: sequences of --seq tokens")
         r.add_argument("--heads", type=int, default=4, help="prefill_reference: Hq = Hkv")
         r.add_argument("--steps", type=int, default=30)
         r.add_argument("--warmup", type=int, default=5)

@@ -123,10 +123,9 @@ def test_decode_stream_many_short_caches(cuda, causal):
 
 
 def test_decode_stream_one_cache_over_all_waves(cuda):
-    """One 70,000-key cache per kv head: 2,188 steps each over 548 waves (the
-    small-call cap, max(128, steps / 8) waves per cache), so every wave holds a
-    piece and the merge of a head sums ~275 partials (four combine workgroups
-    per head, each over a quarter of the row)."""
+    """One 70,000-key cache per kv head: 2,188 steps each over 896 waves, so
+    every wave holds a piece and the merge of a head sums ~449 partials (four
+    combine workgroups per head, each over a quarter of the row)."""
     case = testing.make_case("dec_long", [1], [70000], 8, 2, 128, torch.bfloat16, seed=13,
                              causal=False)
     _check(_decode(case, cuda), _oracle(case))

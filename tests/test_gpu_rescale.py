@@ -33,7 +33,7 @@ RESCALE_LOG2 = 8.0
 WAVE_COUNTS = (896, 2048)  # contiguous 16-bit; paged or fp8 (the tile table)
 # the table's small-call caps: steps per wave; waves per cache (or one per
 # PART_STEPS steps of a longer cache)
-MIN_STEPS, MAX_PARTS, PART_STEPS = 2, 128, 8
+MIN_STEPS, MAX_PARTS, PART_STEPS = 2, 128, 2
 LENS_K = [30000, 1, 7000, 16384, 33, 12000, 64, 20000, 9001, 5000, 31000, 2500]
 
 
