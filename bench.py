@@ -262,6 +262,28 @@ def decode_small_bench(steps, warmup, shapes=((1, 8192), (1, 32768), (1, 131072)
     return rows
 
 
+def decode_bottom_right_bench(steps, warmup, rel_extent=1024):
+    """The 64-sequence decode batch in the serving convention: the query at key
+    Lk - 1 (bottom-right, causal keeps every key) with a per-token bf16 bias
+    of `rel_extent` (the serving model's global layers: 1024), so the last
+    `rel_extent` keys of every cache carry bias; beside the same call top-left,
+    where no key falls in the band."""
+    import torch
+    from inkling_fa4 import inkling_fa4_rel_attention_decode, testing
+
+    g, lens = testing.decode_lengths()
+    case = testing.make_case("decode_br", [1] * len(lens), lens, 8, 2, 128, torch.bfloat16,
+                             seed=5, causal=True, rel_extent=rel_extent, rel_table=False,
+                             rel_dtype=torch.bfloat16, gen=g)
+    c = case.to("cuda")
+    args = c.args()
+    br = time_gpu(lambda: inkling_fa4_rel_attention_decode(
+        *args, causal=True, softmax_scale=c.scale, bottom_right=True), steps, warmup)
+    tl = time_gpu(lambda: inkling_fa4_rel_attention_decode(
+        *args, causal=False, softmax_scale=c.scale), steps, warmup)
+    return {"rel_extent": rel_extent, "bottom_right_us": br * 1e3, "top_left_us": tl * 1e3}
+
+
 def decode_bench(steps, warmup, block_size=0, fp8=False):
     """Decode over the 64-sequence batch; block_size > 0: the same keys in a
     paged cache of that block size (blocks in a shuffled physical order);
@@ -535,6 +557,11 @@ def main():
                                 for k, v in d8.items()}
         if not args.no_sweep:  # (kept out of profiling runs: same kernel, other shapes)
             result["decode_small_batch"] = decode_small_bench(args.steps, args.warmup)
+            dbr = decode_bottom_right_bench(args.steps, args.warmup)
+            log(f"decode bottom-right, bf16 bias extent 1024: {dbr['bottom_right_us']:.1f} us "
+                f"(top-left, no key in the band: {dbr['top_left_us']:.1f} us)")
+            result["decode_bottom_right_bias"] = {k: (round(v, 2) if isinstance(v, float) else v)
+                                                  for k, v in dbr.items()}
         if result["value"] is None:
             result["value"] = round(dec["gbps"], 1)
             result["unit"] = "GB/s"

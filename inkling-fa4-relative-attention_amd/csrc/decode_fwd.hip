@@ -389,7 +389,47 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   f32x4_t o[S::kDBlocks];
   u32x4_t qf[S::kKSteps];
 
+  const int rel_esz = p.rel_dtype == 2 ? 4 : 2;  // bytes per bias element
   auto step = [&](const u32x4_t* kr, const u32x4_t* vr, const Cursor& cu, bool last) {
+    const int k0 = step_key0(cu);
+    const int c1 = cu.kend;
+    const int delta = p.bottom_right ? cu.lk - 1 : 1 - cu.lk;  // dist = delta - key (i = 0)
+    const bool tail = k0 + kStep > c1 || k0 < cu.kbeg;
+    // some key of the step lies in the bias band 0 <= dist < rel_extent (the
+    // step's distances run from delta - k0 down to delta - k0 - 31)
+    const bool bias = p.rel_extent > 0 && delta - k0 >= 0 && delta - k0 - (kStep - 1) < p.rel_extent;
+    // Per-token bias of the step: this lane's keys k0 + 16 blk + 4 g + j of head
+    // n, one dword each (a 16-bit element and its neighbour), issued together
+    // before the K/V wait below so that they land with the K/V rows: one buffer
+    // resource over the sequence's bias row (all heads; its base aligned down
+    // to 4 bytes, `rel_skew` the bytes it moved), masked elements past it
+    // (read as zero).  Per-element loads waited for one at a time cost a
+    // bottom-right decode with bias extent 1024 two thirds more time.
+    uint32_t bw[kStep / 16][4];
+    uint32_t rel_skew = 0;
+    if (bias) {
+      const uint64_t row = reinterpret_cast<uint64_t>(p.rel) +
+                           (uint64_t)((int64_t)cu.qs * p.rel_st * rel_esz);
+      rel_skew = (uint32_t)(row & 3u);
+      // size rounded up to whole dwords: the last element's dword is read whole
+      // (its other bytes share that aligned dword, so they stay on its page)
+      const uint32_t bytes =
+          rel_skew + (uint32_t)(((int64_t)(p.n_heads - 1) * p.rel_sh + p.rel_extent) * rel_esz);
+      const rsrc_t rr =
+          make_rsrc_uniform(reinterpret_cast<const void*>(row - rel_skew), (bytes + 3u) & ~3u);
+#pragma unroll
+      for (int blk = 0; blk < kStep / 16; ++blk) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = k0 + 16 * blk + 4 * g + j;
+          const int dist = delta - key;
+          const bool ok = n < g_act && key < c1 && dist >= 0 && dist < p.rel_extent;
+          const uint32_t off =
+              rel_skew + (uint32_t)(((int64_t)(cu.kvh * g_act + n) * p.rel_sh + dist) * rel_esz);
+          bw[blk][j] = buf_load_4(rr, ok ? (off & ~3u) : kOutOfRange);
+        }
+      }
+    }
     if (cu.first) {
       m_run = -INFINITY;
       l_run = 0.f;
@@ -457,11 +497,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
         acc[blk] = E::mfma16(*reinterpret_cast<const u32x4_t*>(krow + 32 * kk), qf[kk], acc[blk]);
     }
 
-    const int k0 = step_key0(cu);
-    const int c1 = cu.kend;
-    const int delta = p.bottom_right ? cu.lk - 1 : 1 - cu.lk;  // dist = delta - key (i = 0)
-    const bool tail = k0 + kStep > c1 || k0 < cu.kbeg;
-    const bool bias = delta - k0 >= 0;  // some key of the step has dist >= 0
     float mx = -INFINITY;
 #pragma unroll
     for (int blk = 0; blk < kStep / 16; ++blk) {
@@ -472,10 +507,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
           const int key = k0 + 16 * blk + 4 * g + j;
           const int dist = delta - key;  // i = 0
           if (bias && n < g_act && key < c1 && dist >= 0 && dist < p.rel_extent) {
-            x += load_rel(p.rel, (int64_t)cu.qs * p.rel_st +
-                                     (int64_t)(cu.kvh * g_act + n) * p.rel_sh + dist,
-                          p.rel_dtype) *
-                 kLog2e;
+            // the element's half of its dword (16-bit types): by its byte offset
+            const uint32_t off =
+                rel_skew + (uint32_t)(((int64_t)(cu.kvh * g_act + n) * p.rel_sh + dist) * rel_esz);
+            const uint32_t w = bw[blk][j];
+            const uint32_t h16 = (w >> (8 * (off & 2u))) & 0xffffu;
+            const float b = p.rel_dtype == 2   ? __uint_as_float(w)
+                            : p.rel_dtype == 0 ? __uint_as_float(h16 << 16)
+                                               : (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+            x += b * kLog2e;
           }
           if (key >= c1 || key < cu.kbeg) x = -INFINITY;
         }

@@ -100,14 +100,6 @@ template <> struct Elem<F16Tag> {
   }
 };
 
-// Bias element of dtype code `rel_dtype` (0 bf16, 1 fp16, 2 fp32) as fp32.
-__device__ __forceinline__ float load_rel(const void* base, int64_t idx, int rel_dtype) {
-  if (rel_dtype == 2) return static_cast<const float*>(base)[idx];
-  uint32_t bits = static_cast<const uint16_t*>(base)[idx];
-  if (rel_dtype == 0) return __uint_as_float(bits << 16);
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
-}
-
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // max(x[lane], x[lane ^ 32]) in every lane.
