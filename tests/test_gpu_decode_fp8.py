@@ -105,3 +105,16 @@ def test_fp8_rejects_what_it_does_not_serve(cuda):
                              causal=False)
     with pytest.raises(ValueError):
         _fp8_decode(case, cuda)
+
+
+@pytest.mark.parametrize("keys", [32768, 131072])
+def test_fp8_one_sequence_split_combine(cuda, keys):
+    """One sequence of an fp8 cache over 2048 waves: ~1,025 partials per
+    (head, sequence) at 32K keys and 128K, merged by four combine workgroups
+    per (head, sequence), each over a quarter of the row, in several rounds of
+    loads.  Against the oracle on the dequantised K/V."""
+    case = testing.make_case("fp8_split", [1], [keys], 8, 2, 128, torch.bfloat16, seed=33,
+                             causal=False)
+    print(f"fp8 one sequence of {keys} keys", flush=True)
+    got, deq = _fp8_decode(case, cuda)
+    _check(got, _oracle(deq))
