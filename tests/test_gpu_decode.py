@@ -155,26 +155,28 @@ def test_decode_one_sequence_split_combine(cuda, keys, head_dim):
     _check(_decode(case, cuda), _oracle(case))
 
 
+@pytest.mark.parametrize("hq,hkv,head_dim", [(8, 2, 128), (8, 1, 64), (4, 4, 128), (16, 1, 128)])
 @pytest.mark.parametrize("rel_dtype", [torch.bfloat16, torch.float16, torch.float32])
-def test_decode_bottom_right_token_bias_views(cuda, rel_dtype):
+def test_decode_bottom_right_token_bias_views(cuda, rel_dtype, hq, hkv, head_dim):
     """Bottom-right decode (the query at key Lk - 1) with a per-token bias of
     extent 1024: the last 1024 keys of every cache carry bias, gathered per
     step as whole dwords from the sequence's bias row.  The bias is passed as
     a view one element into a wider buffer (a 16-bit row then starts 2 bytes
     into a dword) with an odd head stride (R' + 1), so the element's half of
     its dword alternates between heads; caches shorter and longer than the
-    extent, and lengths on step and extent boundaries."""
+    extent, and lengths on step and extent boundaries; GQA groups 1, 4, 8 and
+    16 and d 64."""
     lens = [1, 5, 31, 300, 1023, 1024, 1025, 2049, 4000, 70]
-    case = testing.make_case("dec_brbias", [1] * len(lens), lens, 8, 2, 128, torch.bfloat16,
-                             seed=16, causal=True, rel_extent=1024, rel_table=False,
-                             rel_dtype=rel_dtype, rel_std=1.0)
+    case = testing.make_case("dec_brbias", [1] * len(lens), lens, hq, hkv, head_dim,
+                             torch.bfloat16, seed=16, causal=True, rel_extent=1024,
+                             rel_table=False, rel_dtype=rel_dtype, rel_std=1.0)
     tq, hq, rw = case.rel.shape
     wide = torch.zeros(tq, hq, rw + 1, dtype=rel_dtype)
     wide[:, :, 1:] = case.rel
     c = case.to(cuda)
     rel_view = wide.to(cuda)[:, :, 1:]
     assert rel_view.stride() == (hq * (rw + 1), rw + 1, 1) and rel_view.storage_offset() == 1
-    print(f"bottom-right token bias {rel_dtype}", flush=True)
+    print(f"bottom-right token bias {rel_dtype}, Hq {hq} / Hkv {hkv}, d {head_dim}", flush=True)
     out, lse = inkling_fa4_rel_attention_decode(
         c.q, c.k, c.v, rel_view, c.cu_q, c.cu_k, c.max_q, c.max_k, c.rel_extent, causal=True,
         softmax_scale=c.scale, return_lse=True, bottom_right=True)
