@@ -468,7 +468,7 @@ def main():
         summarize(args.summarize)
         return 0
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
+        print("bench.py measures one GPU: the library has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
         return 2
 
