@@ -88,6 +88,12 @@ int32_t check_args(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr, int kv
       k_rows * a->k_stride_t * kv_esize >= kLimit || k_rows * a->v_stride_t * kv_esize >= kLimit ||
       ((a->max_seqlen_q + kpad) * a->rel_stride_t + a->rel_width) * rel_esize >= kLimit)
     return IFA4_EUNSUPPORTED;
+  // Decode reads the query heads of a GQA group, and the bias of every head of
+  // a token, through one buffer resource each: the head spans too.
+  if ((int64_t)(a->n_heads - 1) * a->q_stride_h * 2 + (int64_t)a->head_dim * 2 >= kLimit ||
+      (a->rel_extent > 0 &&
+       ((int64_t)(a->n_heads - 1) * a->rel_stride_h + a->rel_width) * rel_esize >= kLimit))
+    return IFA4_EUNSUPPORTED;
   return IFA4_OK;
 }
 
