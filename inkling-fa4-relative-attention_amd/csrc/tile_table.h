@@ -115,8 +115,16 @@ inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seq
 // the critical path, so when it exceeds the work one slot would get with
 // perfect balance, every query tile's range is cut into chunks of that many
 // tiles (at least kPrefillMinChunk), one workgroup per chunk, and a second pass
-// merges the chunks' partials by log-sum-exp.  Where it pays (same-session
-// sweeps, per-token bf16 bias of extent 1024, Hq = Hkv, causal):
+// merges the chunks' partials by log-sum-exp.  The chunk is then lengthened
+// until the chunks with work fit the resident slots at once: with the balanced
+// share, a query tile's last chunk is short and the count overshoots the slots
+// a little (528 for one sequence of 4096 over 4 heads), and the few left over
+// ran as a second round.  Fitted, against the balanced share (same session):
+// one sequence over 4 heads, S 4096 / 8192: 61.6 -> 48.6, 141.6 -> 109.5 us;
+// 8 x 1024: 39.5 -> 36.2; 4 x 2048: 59.5 -> 50.0; 2 x 4096 over 4 heads and
+// 1 x 4096 over 8: 90.7 -> 74.2 (S 1024 / 2048 fit already: unchanged).
+// Where splitting pays (same-session sweeps with the balanced share, per-token
+// bf16 bias of extent 1024, Hq = Hkv, causal):
 //   * grids of at most a quarter of the resident slots always: one sequence
 //     over 4 heads, S 1024 / 2048 / 4096: 45.4 -> 22.2, 71.9 -> 31.3,
 //     104.9 -> 65.8 us;
@@ -138,6 +146,16 @@ constexpr int32_t kPrefillMinChunk = 4;
 #endif
 constexpr int64_t kPrefillSplitMaxGrid = IFA4_PREFILL_SPLIT_MAX_GRID;  // kPrefillSlots / 2
 constexpr int64_t kPrefillSplitSmallGrid = 128;                        // kPrefillSlots / 4
+// Chunk length as a percentage of the balanced share (sweep knob).
+#ifndef IFA4_PREFILL_CHUNK_PCT
+#define IFA4_PREFILL_CHUNK_PCT 100
+#endif
+constexpr int64_t kPrefillChunkPct = IFA4_PREFILL_CHUNK_PCT;
+// Lengthen the chunk until every chunk with work is resident at once (1), or
+// keep the balanced share (0; sweep knob).
+#ifndef IFA4_PREFILL_CHUNK_FIT
+#define IFA4_PREFILL_CHUNK_FIT 1
+#endif
 constexpr int64_t kPrefillSplitWideMinTiles = 16;
 
 struct PrefillSplit {
@@ -161,6 +179,21 @@ inline void prefill_tile_work(int64_t lq, int64_t lk, bool causal, int64_t windo
   }
 }
 
+// Chunks with work of one (sequence, head) when the KV range of every query
+// tile is cut at multiples of `chunk` key tiles (the kernel's alignment).
+inline int64_t prefill_chunk_count(int64_t lq, int64_t lk, bool causal, int64_t window_left,
+                                   int32_t block_q, int32_t block_k, int64_t chunk) {
+  int64_t n = 0;
+  for (int64_t q0 = 0; q0 < lq; q0 += block_q) {
+    const int64_t q_hi = q0 + block_q < lq ? q0 + block_q : lq;
+    const int64_t kend = causal ? (q_hi < lk ? q_hi : lk) : lk;
+    const int64_t kbeg = window_left >= 0 ? (q0 - window_left > 0 ? q0 - window_left : 0) : 0;
+    if (kend <= kbeg) continue;
+    n += ((kend + block_k - 1) / block_k - 1) / chunk - (kbeg / block_k) / chunk + 1;
+  }
+  return n;
+}
+
 // forced_chunk > 0: split every query tile into chunks of that many tiles.
 inline PrefillSplit prefill_split_for(int64_t batch, int64_t n_heads, int64_t max_q,
                                       int64_t max_k, bool causal, int64_t window_left,
@@ -174,8 +207,29 @@ inline PrefillSplit prefill_split_for(int64_t batch, int64_t n_heads, int64_t ma
     const int64_t grid = (max_q + block_q - 1) / block_q * n_heads * batch;
     if (grid > kPrefillSplitMaxGrid) return s;
     if (grid > kPrefillSplitSmallGrid && tmax < kPrefillSplitWideMinTiles) return s;
-    const int64_t balanced = (total * batch * n_heads + kPrefillSlots - 1) / kPrefillSlots;
+    const int64_t balanced =
+        ((total * batch * n_heads + kPrefillSlots - 1) / kPrefillSlots * kPrefillChunkPct + 99) /
+        100;
     chunk = balanced > kPrefillMinChunk ? balanced : kPrefillMinChunk;
+    if (IFA4_PREFILL_CHUNK_FIT && chunk < tmax) {
+      // Chunks of the balanced share can number a little more than the slots
+      // (each query tile's last chunk is short): the few left over then run as
+      // a second round.  Take the shortest chunk whose workgroups all fit
+      // (binary search; the count falls as the chunk grows).
+      auto fits = [&](int64_t c) {
+        return prefill_chunk_count(max_q, max_k, causal, window_left, block_q, block_k, c) *
+                   batch * n_heads <=
+               kPrefillSlots;
+      };
+      if (!fits(chunk)) {
+        int64_t lo = chunk, hi = tmax;  // fits(hi): one chunk per query tile, grid <= slots
+        while (hi - lo > 1) {
+          const int64_t mid = lo + (hi - lo) / 2;
+          if (fits(mid)) hi = mid; else lo = mid;
+        }
+        chunk = hi;
+      }
+    }
     if (tmax <= chunk) return s;
   }
   // chunk slots: enough for a query tile that meets every key tile (chunks are

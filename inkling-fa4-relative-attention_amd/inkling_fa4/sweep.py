@@ -52,6 +52,7 @@ Knobs (macros of the kernel sources):
                    IFA4_DECODE_WAVES_FP8      the same for an fp8 KV cache (workload decode_fp8)
                    IFA4_DECODE_WAVES_PAGED    the same for a paged cache (workload decode_paged)
                    IFA4_PREFILL_SPLIT_MAX_GRID  largest prefill grid the table splits (split KV)
+                   IFA4_PREFILL_CHUNK_PCT     split KV: chunk length, percent of the balanced share
 """
 import argparse
 import hashlib
