@@ -133,8 +133,16 @@ inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seq
 //     16 tiles) 53.4 -> 43.3 us, 4 x 2048 73.1 -> 63.7, 1 x 8192 172.5 -> 147.7;
 //     with 8-tile ranges the merge costs more than it saves (16 x 512: 30.6 ->
 //     31.9 us; the shared-table 8 x 512 over 8 heads: 18.0 -> 28.8);
-//   * never above: every grid of 512 workgroups measured lost (8 x 1024 over 8
-//     heads 32.0 -> 45.6 us, 1 x 16384 over 4 heads 373 -> 447, 2 x 8192 206 -> 225).
+//   * with fitted chunks, grids below the slots too, when the chunk is at most
+//     half of the longest range or shortens it by kPrefillSplitMinSaved tiles
+//     (against no split, same session): 3 x 4096 over 4 heads (384 workgroups,
+//     chunk 44 of 64 tiles) 112.3 -> 104.8 us, 5 x 2048 (16 of 32) 71.4 ->
+//     61.5, 1 x 8192 over 6 (86 of 128) 185.5 -> 170.3, 5 x 1024 over 8 (8 of
+//     16) 48.2 -> 41.5; at 22 of 32 (6 x 2048, 3 x 2048 over 8) equal, at 12 of
+//     16 (12 x 1024) 1% slower, at 14 of 16 (7 x 1024 over 8) 12% slower;
+//   * never at the slots and above: every grid of 512 workgroups measured lost
+//     (8 x 1024 over 8 heads 32.0 -> 45.6 us, 1 x 16384 over 4 heads 373 -> 447,
+//     2 x 8192 206 -> 225), and no chunk fits the slots there.
 // The estimate assumes every sequence holds max_seqlen_q queries over
 // max_seqlen_k keys (top-left); it only steers performance, any chunk size
 // gives the same results up to rounding.  kPrefillSlots: resident workgroups
@@ -142,9 +150,15 @@ inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seq
 constexpr int64_t kPrefillSlots = 512;
 constexpr int32_t kPrefillMinChunk = 4;
 #ifndef IFA4_PREFILL_SPLIT_MAX_GRID
-#define IFA4_PREFILL_SPLIT_MAX_GRID 256
+#define IFA4_PREFILL_SPLIT_MAX_GRID 511
 #endif
-constexpr int64_t kPrefillSplitMaxGrid = IFA4_PREFILL_SPLIT_MAX_GRID;  // kPrefillSlots / 2
+constexpr int64_t kPrefillSplitMaxGrid = IFA4_PREFILL_SPLIT_MAX_GRID;  // below kPrefillSlots
+// A split is taken when its chunk is at most half of the longest KV range, or
+// shortens that range by at least this many tiles.
+#ifndef IFA4_PREFILL_SPLIT_MIN_SAVED
+#define IFA4_PREFILL_SPLIT_MIN_SAVED 16
+#endif
+constexpr int64_t kPrefillSplitMinSaved = IFA4_PREFILL_SPLIT_MIN_SAVED;
 constexpr int64_t kPrefillSplitSmallGrid = 128;                        // kPrefillSlots / 4
 // Chunk length as a percentage of the balanced share (sweep knob).
 #ifndef IFA4_PREFILL_CHUNK_PCT
@@ -222,7 +236,10 @@ inline PrefillSplit prefill_split_for(int64_t batch, int64_t n_heads, int64_t ma
                kPrefillSlots;
       };
       if (!fits(chunk)) {
-        int64_t lo = chunk, hi = tmax;  // fits(hi): one chunk per query tile, grid <= slots
+        // hi = tmax: one chunk per query tile whose range starts at key 0, which
+        // the grid (below the slots) fits; otherwise the search ends there and
+        // the call is not split
+        int64_t lo = chunk, hi = tmax;
         while (hi - lo > 1) {
           const int64_t mid = lo + (hi - lo) / 2;
           if (fits(mid)) hi = mid; else lo = mid;
@@ -230,7 +247,9 @@ inline PrefillSplit prefill_split_for(int64_t batch, int64_t n_heads, int64_t ma
         chunk = hi;
       }
     }
-    if (tmax <= chunk) return s;
+    // A split that shortens the longest range by little does not repay the
+    // chunks' partials and the merge pass.
+    if (tmax <= chunk || (2 * chunk > tmax && tmax - chunk < kPrefillSplitMinSaved)) return s;
   }
   // chunk slots: enough for a query tile that meets every key tile (chunks are
   // aligned to multiples of `chunk` tiles on the key axis), so the grid and the

@@ -109,6 +109,20 @@ def test_split_plan_on_the_host():
     assert _workspace_bytes(8, 8, 2, 512)[0] == 0
     # 512 workgroups never split
     assert _workspace_bytes(1, 4, 4, 16384)[0] == 0
+    # below the slots the chunk is lengthened until the chunks with work fit
+    # them at once; the split is taken at half the longest range or less, or
+    # when it saves 16 tiles or more
+    chunk = lambda batch, heads, seq: _abi.prefill_tile(  # noqa: E731
+        128, batch=batch, n_heads=heads, seq_len=seq).kv_chunk // 64
+    assert chunk(1, 4, 4096) == 10    # balanced share 9: 528 chunks, 10: 476
+    assert chunk(1, 4, 8192) == 43    # 33: 632 chunks, 43: 512
+    assert chunk(5, 4, 2048) == 16    # 320 workgroups, ranges of 32 tiles
+    assert chunk(3, 4, 4096) == 44    # 384 workgroups, saves 20 of 64 tiles
+    assert _workspace_bytes(5, 4, 4, 2048)[0] > 0
+    assert _workspace_bytes(3, 4, 4, 4096)[0] > 0
+    assert _workspace_bytes(12, 4, 4, 1024)[0] == 0  # 12 of 16 tiles
+    assert _workspace_bytes(6, 4, 4, 2048)[0] == 0   # 22 of 32 tiles
+    assert _workspace_bytes(7, 8, 8, 1024)[0] == 0   # 14 of 16 tiles
     # the test flag splits everything with more than two tiles per query tile
     assert _workspace_bytes(8, 8, 2, 4096, flags=SPLIT2)[0] > 0
 
