@@ -89,6 +89,9 @@
 #ifndef IFA4_PROJ_EARLY
 #define IFA4_PROJ_EARLY 1
 #endif
+#ifndef IFA4_MERGE_BATCH
+#define IFA4_MERGE_BATCH 4
+#endif
 
 namespace ifa4 {
 namespace {
@@ -1125,7 +1128,7 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillPar
   }
   // kChunkBatch chunks per round: every load of a round (its rows x chunks)
   // is issued before the first is used
-  constexpr int kChunkBatch = 4;
+  constexpr int kChunkBatch = IFA4_MERGE_BATCH;
   for (int c0 = 0; c0 < nch; c0 += kChunkBatch) {
     float ls[kChunkBatch][kRows];
     float os[kChunkBatch][kRows][kPer];

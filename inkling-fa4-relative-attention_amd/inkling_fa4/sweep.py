@@ -41,6 +41,8 @@ Knobs (macros of the kernel sources):
                                               the band (0/1; workloads rproj128/512/1024)
                    IFA4_PROJ_EARLY            fused projection: key block 0's distances
                                               projected before the QK products (0/1)
+                   IFA4_MERGE_BATCH           split-KV merge pass: chunks whose loads are in
+                                              flight together (2/4/8)
   ifa4_device.hpp  IFA4_DMA_COVER_EACH        hazard cover on every LDS DMA (1) or one per
                                               batch of a tile's DMAs (0)
   decode_fwd.hip   IFA4_DECODE_WPE            waves per SIMD the stream pass's registers target
