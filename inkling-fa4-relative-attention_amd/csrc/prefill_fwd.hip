@@ -92,6 +92,12 @@
 #ifndef IFA4_MERGE_BATCH
 #define IFA4_MERGE_BATCH 4
 #endif
+#ifndef IFA4_MERGE_PARTS
+#define IFA4_MERGE_PARTS 8
+#endif
+#ifndef IFA4_MERGE_THREADS
+#define IFA4_MERGE_THREADS 256
+#endif
 
 namespace ifa4 {
 namespace {
@@ -1090,14 +1096,16 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
 }
 
 // Merge of split-KV partials (second pass after a split launch): kMergeParts
-// workgroups per (q tile, head, sequence), each a quarter of the tile's rows; a
+// workgroups per (q tile, head, sequence), each an eighth of the tile's rows
+// (against a quarter: 1.3% faster on one sequence of 4096 over 4 heads, 3% at
+// 2048, within 1% elsewhere; sixteenths no better); a
 // tile whose range did not split was written by the prefill kernel itself and
 // is skipped.  32 threads share a row (head_dim / 32 consecutive d values each)
 // and a thread holds kRows rows; chunks go in rounds of kChunkBatch whose loads
 // (rows x chunks) are all in flight at once, merged online (running max over
 // the chunks' LSEs).
-constexpr int kMergeThreads = 256;
-constexpr int kMergeParts = 4;
+constexpr int kMergeThreads = IFA4_MERGE_THREADS;
+constexpr int kMergeParts = IFA4_MERGE_PARTS;
 template <typename Sh, int D, typename Tag>
 __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillParams p) {
   using E = Elem<Tag>;
@@ -1105,6 +1113,8 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillPar
   constexpr int kPer = D / kTpr;                    // d values per thread
   constexpr int kStride = kMergeThreads / kTpr;     // rows per pass of the workgroup
   constexpr int kRows = Sh::kBlockQ / kMergeParts / kStride;  // rows per thread
+  static_assert(kRows >= 1 && kRows * kStride * kMergeParts == Sh::kBlockQ,
+                "merge workgroups cover the query tile's rows exactly");
   const int qtile = blockIdx.x / kMergeParts, part = blockIdx.x % kMergeParts;
   const int head = blockIdx.y, seq = blockIdx.z;
   const SeqBounds bq = seq_bounds(p.cu_q, seq, p.total_q);

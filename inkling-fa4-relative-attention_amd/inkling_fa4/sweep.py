@@ -43,6 +43,8 @@ Knobs (macros of the kernel sources):
                                               projected before the QK products (0/1)
                    IFA4_MERGE_BATCH           split-KV merge pass: chunks whose loads are in
                                               flight together (2/4/8)
+                   IFA4_MERGE_PARTS           split-KV merge pass: workgroups per query tile
+                                              (4/8/16)
   ifa4_device.hpp  IFA4_DMA_COVER_EACH        hazard cover on every LDS DMA (1) or one per
                                               batch of a tile's DMAs (0)
   decode_fwd.hip   IFA4_DECODE_WPE            waves per SIMD the stream pass's registers target
