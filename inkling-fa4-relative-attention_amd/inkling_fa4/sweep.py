@@ -57,6 +57,7 @@ Knobs (macros of the kernel sources):
                    IFA4_DECODE_WAVES_PAGED    the same for a paged cache (workload decode_paged)
                    IFA4_PREFILL_SPLIT_MAX_GRID  largest prefill grid the table splits (split KV)
                    IFA4_PREFILL_CHUNK_PCT     split KV: chunk length, percent of the balanced share
+                   IFA4_PREFILL_MIN_CHUNK     split KV: shortest chunk in KV tiles
                    IFA4_PREFILL_CHUNK_FIT     split KV: chunk lengthened until the chunks fit the
                                               resident slots (0/1)
                    IFA4_PREFILL_SPLIT_MIN_SAVED  split KV taken for chunks over half the longest
