@@ -1122,7 +1122,8 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillPar
   const int q0 = qtile * Sh::kBlockQ;
   if (q0 >= bq.len) return;
   const int qpos = p.bottom_right ? bk.len - bq.len : 0;
-  const int nch = tile_chunks(p, tile_range<Sh>(p, q0, bq.len, bk.len, qpos));
+  const TileRange tr = tile_range<Sh>(p, q0, bq.len, bk.len, qpos);
+  const int nch = tile_chunks(p, tr);
   if (nch <= 1) return;
   const int r0 = q0 + part * (Sh::kBlockQ / kMergeParts) + (int)threadIdx.x / kTpr;
   const int d0 = ((int)threadIdx.x % kTpr) * kPer;
@@ -1139,7 +1140,12 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillPar
   // kChunkBatch chunks per round: every load of a round (its rows x chunks)
   // is issued before the first is used
   constexpr int kChunkBatch = IFA4_MERGE_BATCH;
-  for (int c0 = 0; c0 < nch; c0 += kChunkBatch) {
+  // Rounds start at absolute chunk indices that are multiples of kChunkBatch
+  // (slot k of this query tile is absolute chunk tr.beg / chunk_tiles + k), so
+  // the chunks meet in the same rounds whatever the pruning: chunks a pruned
+  // range drops hold no key (LSE -inf) and leave the running sums bit-unchanged.
+  const int lead = (tr.beg / p.chunk_tiles) % kChunkBatch;
+  for (int c0 = -lead; c0 < nch; c0 += kChunkBatch) {
     float ls[kChunkBatch][kRows];
     float os[kChunkBatch][kRows][kPer];
 #pragma unroll
@@ -1147,8 +1153,8 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillPar
 #pragma unroll
       for (int i = 0; i < kRows; ++i) {
         const int row = r0 + kStride * i;
-        const bool ok = row < bq.len && c0 + cb < nch;
-        const int64_t prow = (c0 + cb) * chunk_rows + row0 + row;
+        const bool ok = row < bq.len && c0 + cb >= 0 && c0 + cb < nch;
+        const int64_t prow = (ok ? c0 + cb : 0) * chunk_rows + row0 + row;
         ls[cb][i] = ok ? p.part_lse[prow] : -INFINITY;
         if constexpr (kPer == 4) {
           const f32x4_t v =

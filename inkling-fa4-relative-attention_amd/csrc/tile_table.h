@@ -148,12 +148,11 @@ inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seq
 // gives the same results up to rounding.  kPrefillSlots: resident workgroups
 // of the prefill kernel on MI355X (256 CUs x 2).
 constexpr int64_t kPrefillSlots = 512;
-// Shortest chunk (sweep knob).  2 tiles measured faster than 4 on one sequence
-// over 4 heads (S 384 / 512 / 1024: 18.6 -> 14.3, 18.5 -> 14.7, 20.4 -> 18.8
-// us), but then a pruned and an unpruned launch of one bottom-right windowed
-// case differ in their last bits; kept at 4 until that is understood.
+// Shortest chunk: 2 tiles (against 4, one sequence over 4 heads, same session:
+// S 384 / 512 / 1024 18.6 -> 14.3, 18.5 -> 14.7, 20.4 -> 18.8 us; 3 tiles in
+// between).
 #ifndef IFA4_PREFILL_MIN_CHUNK
-#define IFA4_PREFILL_MIN_CHUNK 4
+#define IFA4_PREFILL_MIN_CHUNK 2
 #endif
 constexpr int32_t kPrefillMinChunk = IFA4_PREFILL_MIN_CHUNK;
 #ifndef IFA4_PREFILL_SPLIT_MAX_GRID
