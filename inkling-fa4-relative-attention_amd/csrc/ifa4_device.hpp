@@ -217,28 +217,29 @@ __device__ __forceinline__ void dma_16(rsrc_t r, uint32_t byte_off, const void* 
                : "memory");
 }
 
-// Same DMA with the wave-uniform part of the offset in the instruction's scalar
-// offset (soffset) and the LDS byte address already in an SGPR value: the
-// caller keeps the per-lane offset in a register across tiles and does the
-// per-tile arithmetic on the scalar unit.  Each DMA carries its own hazard
-// cover (s_nop 4: 5 wait states, enough for a VALU write of the resource, the
-// soffset or M0 and for the SALU write of M0), so no instruction the compiler
-// schedules between two DMAs can expose one.  IFA4_DMA_COVER_EACH=0 (a sweep
-// knob) restores the earlier form, one s_nop 4 per batch issued by the caller
-// and s_nop 0 here, which is only safe while no VALU writes those SGPRs inside
-// the batch.
+// Same DMA through a resource the caller builds per tile (its base at the
+// tile's first row, its size ending where the sequence's rows end), with the
+// per-lane offset kept in a register across tiles and the LDS byte address
+// already in an SGPR value.  The buffer range check on gfx9 covers the per-lane
+// and instruction offsets only, not the scalar offset, so the tile's start must
+// be in the resource base for rows past the sequence end to read as zero.
+// Each DMA carries its own hazard cover (s_nop 4: 5 wait states, enough for a
+// VALU write of the resource or M0 and for the SALU write of M0), so no
+// instruction the compiler schedules between two DMAs can expose one.
+// IFA4_DMA_COVER_EACH=0 (a sweep knob) restores the earlier form, one s_nop 4
+// per batch issued by the caller and s_nop 0 here, which is only safe while no
+// VALU writes those SGPRs inside the batch.
 #ifndef IFA4_DMA_COVER_EACH
 #define IFA4_DMA_COVER_EACH 1
 #endif
-__device__ __forceinline__ void dma_16_so(rsrc_t r, uint32_t lane_off, uint32_t soffset,
-                                          uint32_t lds_addr) {
+__device__ __forceinline__ void dma_16_tile(rsrc_t r, uint32_t lane_off, uint32_t lds_addr) {
 #if IFA4_DMA_COVER_EACH
-  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(lane_off), "s"(r),
-               "s"(soffset), "{m0}"(lds_addr)
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(lane_off), "s"(r),
+               "{m0}"(lds_addr)
                : "memory");
 #else
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(lane_off), "s"(r),
-               "s"(soffset), "{m0}"(lds_addr)
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(lane_off), "s"(r),
+               "{m0}"(lds_addr)
                : "memory");
 #endif
 }

@@ -336,8 +336,8 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   const uint16_t* v_base = static_cast<const uint16_t*>(p.v) + (int64_t)ks * p.v_st +
                            (int64_t)kvh * p.v_sh;
   const rsrc_t rq = make_rsrc(q_base, span_bytes(lq, p.q_st, D, 2));
-  const rsrc_t rk = make_rsrc(k_base, span_bytes(lk, p.k_st, D, 2));
-  const rsrc_t rv = make_rsrc(v_base, span_bytes(lk, p.v_st, D, 2));
+  [[maybe_unused]] const rsrc_t rk = make_rsrc(k_base, span_bytes(lk, p.k_st, D, 2));
+  [[maybe_unused]] const rsrc_t rv = make_rsrc(v_base, span_bytes(lk, p.v_st, D, 2));
   const uint32_t k_row = (uint32_t)p.k_st * 2, v_row = (uint32_t)p.v_st * 2;
 
   // ---- key range of the workgroup (tile pruning, then this KV chunk) ---------
@@ -394,14 +394,17 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   const int dma_slot = lane % St::kChunks;
 #if IFA4_DMA2
   // Each wave DMAs rows of one tensor (K for the first half of the waves, V for
-  // the second).  A lane's offset within a DMA depends on the tile only through
-  // kb (the scalar offset, one multiply per tile): one register per DMA of the
-  // wave (its tile row's offset and swizzled chunk), set once.
+  // the second).  A lane's offset within a DMA is relative to the tile's first
+  // row: one register per DMA of the wave (its tile row's offset and swizzled
+  // chunk), set once.  The tile's start goes into the base of a resource built
+  // per tile (scalar arithmetic), whose size ends with the sequence's last row,
+  // so rows of a partial last tile past the sequence end read as zero.
   static_assert(St::kDmaPerWave <= St::kDmaPerTensor && St::kDmaPerTensor % St::kDmaPerWave == 0,
                 "a wave's DMAs stay within one tensor");
   const bool dma_v = wave * St::kDmaPerWave >= St::kDmaPerTensor;
   const uint32_t dma_rowb = dma_v ? v_row : k_row;
-  const rsrc_t dma_r = dma_v ? rv : rk;
+  const char* const dma_base = reinterpret_cast<const char*>(dma_v ? v_base : k_base);
+  const uint32_t dma_span = span_bytes(lk, dma_v ? p.v_st : p.k_st, D, 2);
   uint32_t dma_voff[St::kDmaPerWave];
 #pragma unroll
   for (int u = 0; u < St::kDmaPerWave; ++u) {
@@ -414,14 +417,15 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   auto dma_tile = [&](int kt, uint16_t* stage) {
     const int kb = kt * kBlockK;
     const uint32_t stage_lds = lds_stages + (uint32_t)((stage - stages) * 2);
+    const uint32_t skip = (uint32_t)kb * dma_rowb;  // bytes before the tile's first row
+    const rsrc_t r = make_rsrc_uniform(dma_base + skip, dma_span > skip ? dma_span - skip : 0u);
     if (!IFA4_DMA_COVER_EACH) hazard_nop5();  // batch cover (sweep knob)
-    const uint32_t soff = (uint32_t)kb * dma_rowb;  // the tile's first row
 #pragma unroll
     for (int u = 0; u < St::kDmaPerWave; ++u) {
       const int id = wave * St::kDmaPerWave + u;
       const int blk = dma_v ? id - St::kDmaPerTensor : id;
       const uint32_t dst = stage_lds + (uint32_t)(((dma_v ? St::kTile : 0) + blk * 512) * 2);
-      dma_16_so(dma_r, dma_voff[u], soff, dst);
+      dma_16_tile(r, dma_voff[u], dst);
     }
   };
 #else
