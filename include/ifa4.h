@@ -297,6 +297,10 @@ int32_t ifa4_decode_quant_fwd(const ifa4_args* args, const ifa4_paged_kv* kv,
  * that GPU's array, so calls that overlap in time on one GPU (other streams or
  * host threads) race.  `stream` must belong to the current device (else
  * IFA4_EINVAL).  Results are those of ifa4_decode_fwd on the same arguments.
+ * The array's device address is looked up on the first call on each device and
+ * kept for the rest of the process: after hipDeviceReset on a device (or an
+ * unload of the library) the kept address is stale, so the entry point must not
+ * be called there again.
  */
 #define IFA4_DECODE_SCRATCH_BYTES (32u << 20)
 int32_t ifa4_decode_fwd_noalloc(const ifa4_args* args, void* stream);

@@ -88,8 +88,16 @@ int32_t check_args(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr, int kv
       k_rows * a->k_stride_t * kv_esize >= kLimit || k_rows * a->v_stride_t * kv_esize >= kLimit ||
       ((a->max_seqlen_q + kpad) * a->rel_stride_t + a->rel_width) * rel_esize >= kLimit)
     return IFA4_EUNSUPPORTED;
-  // Decode reads the query heads of a GQA group, and the bias of every head of
-  // a token, through one buffer resource each: the head spans too.
+  return IFA4_OK;
+}
+
+// Decode reads the query heads of a GQA group, and the bias of every head of a
+// token, through one buffer resource each: their spans over the heads must stay
+// below 2 GiB too.  Prefill addresses each head from its own 64-bit base and
+// has no such limit.
+int32_t check_head_spans(const ifa4_args* a) {
+  const int64_t kLimit = int64_t(1) << 31;
+  const int64_t rel_esize = a->rel_dtype == IFA4_FP32 ? 4 : 2;
   if ((int64_t)(a->n_heads - 1) * a->q_stride_h * 2 + (int64_t)a->head_dim * 2 >= kLimit ||
       (a->rel_extent > 0 &&
        ((int64_t)(a->n_heads - 1) * a->rel_stride_h + a->rel_width) * rel_esize >= kLimit))
@@ -231,6 +239,7 @@ int32_t check_decode(const ifa4_args* a, const ifa4_paged_kv* kv = nullptr,
   if (qt != nullptr && (st = check_quant(qt)) != IFA4_OK) return st;
   const int esize = qt != nullptr ? 1 : 2;
   if ((st = check_args(a, kv, esize)) != IFA4_OK) return st;
+  if ((st = check_head_spans(a)) != IFA4_OK) return st;
   if (kv != nullptr && (st = check_paged(a, kv, esize)) != IFA4_OK) return st;
   if (qt != nullptr && a->n_heads / a->kv_heads > ifa4::decode_fp8_max_group())
     return IFA4_EUNSUPPORTED;

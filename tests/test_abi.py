@@ -134,19 +134,33 @@ def test_validate_span_limits():
     assert _validate(**dict(ok, max_seqlen_q=lr)) == _abi.IFA4_EUNSUPPORTED
 
 
-def test_validate_head_span_limits():
+def _decode_ws(**kw):
+    a = _good(batch=2, total_q=2, max_seqlen_q=1, **kw)
+    return _abi.lib().ifa4_decode_workspace_bytes(ctypes.byref(a))
+
+
+def test_decode_head_span_limits():
     """Decode addresses the bias of all heads of a token, and the query heads
     of a GQA group, through one buffer resource each: the span over the heads
     must stay below 2 GiB as well.  8 heads, fp32 bias of width 128, bf16 q of
-    head_dim 128; one step on each side of the limit."""
+    head_dim 128; one step on each side of the limit.  Prefill addresses every
+    head from its own base: head-major layouts past 2 GiB still validate."""
     sh = -(-((1 << 31) // 4 - 128) // 7)  # smallest rel_stride_h with (7 sh + 128) * 4 >= 2 GiB
-    assert _validate(rel_stride_h=sh - 1) == _abi.IFA4_OK
-    assert _validate(rel_stride_h=sh) == _abi.IFA4_EUNSUPPORTED
-    assert _validate(rel_stride_h=sh, rel_extent=0, rel=0) == _abi.IFA4_OK  # no bias read
+    assert _decode_ws(rel_stride_h=sh - 1) > 0
+    assert _decode_ws(rel_stride_h=sh) == 0
+    assert _decode_ws(rel_stride_h=sh, rel_extent=0, rel=0) > 0  # no bias read
     ql = -(-((1 << 31) // 2 - 128) // 7)  # smallest q_stride_h with 7 ql * 2 + 256 >= 2 GiB
     qh = -(-ql // 8) * 8  # the first multiple of 8 (16-byte rows) at or past it
-    assert _validate(q_stride_h=qh - 8) == _abi.IFA4_OK
-    assert _validate(q_stride_h=qh) == _abi.IFA4_EUNSUPPORTED
+    assert _decode_ws(q_stride_h=qh - 8) > 0
+    assert _decode_ws(q_stride_h=qh) == 0
+    lib = _abi.lib()
+    a = _good(batch=2, total_q=2, max_seqlen_q=1, q_stride_h=qh)
+    assert lib.ifa4_decode_fwd(ctypes.byref(a), 256, 1 << 30, None) == _abi.IFA4_EUNSUPPORTED
+    # prefill: q as the transpose of a head-major [H, T, D] tensor of >= 2 GiB
+    assert _validate(q_stride_h=qh) == _abi.IFA4_OK
+    assert _validate(rel_stride_h=sh) == _abi.IFA4_OK
+    t = 1 << 21  # tokens: 8 heads x 2M tokens x 128 x 2 bytes = 4 GiB
+    assert _validate(q_stride_t=128, q_stride_h=t * 128, total_q=t) == _abi.IFA4_OK
 
 
 def test_launch_entry_points_reject_bad_args_before_any_launch():
