@@ -101,7 +101,7 @@ def time_gpu_samples(fn, steps, warmup):
     return sorted(a.elapsed_time(b) for a, b in evs)
 
 
-def prefill_bench(seq_len, steps, warmup, batch=8):
+def prefill_bench(seq_len, steps, warmup, batch=8, samples=True):
     import torch
     from inkling_fa4 import inkling_fa4_rel_attention, testing
 
@@ -118,7 +118,7 @@ def prefill_bench(seq_len, steps, warmup, batch=8):
         return inkling_fa4_rel_attention(*args, causal=True, softmax_scale=c.scale)
 
     ms = time_gpu(step, steps, warmup)
-    samples = time_gpu_samples(step, max(10, min(steps, 50)), 2)
+    samples = time_gpu_samples(step, max(10, min(steps, 50)), 2) if samples else [ms]
     tflops = flops / (ms * 1e-3) / 1e12
     return {
         "seq_len": seq_len, "batch": batch, "ms": ms, "tflops": tflops,
@@ -428,26 +428,42 @@ def copy_loop(n_bytes=256 << 20, reps=5):
     log(f"copied {reps} x {n_bytes} bytes")
 
 
-def summarize(db_path):
+def summarize(db_path, last=None):
     """Print per-kernel dispatch statistics and per-dispatch counter averages
-    from a rocprofv3 output database (SQLite)."""
+    from a rocprofv3 output database (SQLite).  With `last`, each kernel's
+    figures cover only its last `last` dispatches (by start time): the timed
+    steps of a `--no-samples` run, without the clock-settling calls before
+    them."""
     import sqlite3
 
     con = sqlite3.connect(db_path)
-    print(f"profile: {db_path}")
-    print("| kernel | calls | avg us | total us | % |")
-    print("|---|---|---|---|---|")
-    for name, n, tot, avg, pct in con.execute(
-            "select name, total_calls, total_duration, average, percentage from top_kernels"):
-        print(f"| {name} | {n} | {avg:.3f} | {tot:.1f} | {pct:.1f} |")
-    rows = list(con.execute("select kernel_name, counter_name, avg(value), count(*) "
-                            "from counters_collection group by kernel_name, counter_name"))
-    if rows:
+    print(f"profile: {db_path}" + (f" (last {last} dispatches of each kernel)" if last else ""))
+    print("| kernel | calls | avg us | min us | max us | total us |")
+    print("|---|---|---|---|---|---|")
+    keep = {}  # kernel name -> dispatch ids summarised
+    for (name,) in con.execute("select distinct name from kernels"):
+        rows = list(con.execute("select dispatch_id, duration from kernels where name = ? "
+                                "order by start", (name,)))
+        if last:
+            rows = rows[-last:]
+        keep[name] = {r[0] for r in rows}
+        d = [r[1] / 1e3 for r in rows]
+        print(f"| {name} | {len(d)} | {sum(d) / len(d):.3f} | {min(d):.3f} | {max(d):.3f} "
+              f"| {sum(d):.1f} |")
+    per = {}  # (kernel, counter) -> {dispatch: value}
+    for k, cn, did, v in con.execute("select kernel_name, counter_name, dispatch_id, value "
+                                     "from counters_collection"):
+        if last and did not in keep.get(k, ()):
+            continue
+        cell = per.setdefault((k, cn), {})
+        cell[did] = cell.get(did, 0.0) + v
+    if per:
         print()
         print("| kernel | counter | per-dispatch avg | dispatches |")
         print("|---|---|---|---|")
-        for k, cn, v, n in rows:
-            print(f"| {k} | {cn} | {v:.6g} | {n} |")
+        for (k, cn), cell in sorted(per.items()):
+            vals = list(cell.values())
+            print(f"| {k} | {cn} | {sum(vals) / len(vals):.6g} | {len(vals)} |")
 
 
 def main():
@@ -461,11 +477,16 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--summarize", metavar="DB",
                     help="print a rocprofv3 output database as markdown tables and exit")
+    ap.add_argument("--last", type=int, default=None,
+                    help="with --summarize: only each kernel's last N dispatches")
+    ap.add_argument("--no-samples", action="store_true",
+                    help="skip the per-call timing samples after the timed steps (profiling "
+                         "runs: the timed steps are then each kernel's last dispatches)")
     ap.add_argument("--copy-only", action="store_true",
                     help="only run device copies of a known size (counter calibration)")
     args = ap.parse_args()
     if args.summarize:
-        summarize(args.summarize)
+        summarize(args.summarize, args.last)
         return 0
     if args.gpus != 1:
         print("bench.py measures one GPU: the library has no multi-GPU path "
@@ -497,7 +518,8 @@ def main():
     case = None
     if args.only in ("all", "prefill"):
         log(f"prefill seq {args.seq}: {args.steps} steps")
-        pre, case = prefill_bench(args.seq, args.steps, args.warmup)
+        pre, case = prefill_bench(args.seq, args.steps, args.warmup,
+                                  samples=not args.no_samples)
         log(f"prefill seq {args.seq}: {pre['ms']:.4f} ms  {pre['tflops']:.1f} TFLOP/s")
         result["value"] = round(pre["tflops"], 2)
         result["ms_per_step"] = round(pre["ms"], 5)
