@@ -160,7 +160,9 @@ ifa4::PrefillParams make_prefill_params(const ifa4_args* a) {
   p.group = a->n_heads / a->kv_heads;
   p.rel_extent = a->rel_extent;
   p.rel_width = a->rel_width;
-  p.window_left = a->window_left;
+  // any window of 2^30 keys or more covers every sequence (rows stay below 2^31
+  // bytes / 256-byte rows): clamped so that index arithmetic on it stays in int32
+  p.window_left = a->window_left < (1 << 30) ? a->window_left : (1 << 30);
   p.causal = a->causal;
   p.bottom_right = (a->flags & IFA4_FLAG_BOTTOM_RIGHT) ? 1 : 0;
   p.no_prune = (a->flags & IFA4_FLAG_NO_PRUNE) ? 1 : 0;
@@ -290,7 +292,7 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
   p.rel_extent = args->rel_extent;
   p.causal = args->causal;
   p.bottom_right = (args->flags & IFA4_FLAG_BOTTOM_RIGHT) ? 1 : 0;
-  p.window_left = args->window_left;
+  p.window_left = args->window_left < (1 << 30) ? args->window_left : (1 << 30);
   p.rel_dtype = args->rel_dtype;
   p.n_waves = decode_waves(args, qt != nullptr, kv != nullptr);
   p.kv_fp8 = qt != nullptr ? 1 : 0;

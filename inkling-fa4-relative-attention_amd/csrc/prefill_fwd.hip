@@ -113,7 +113,9 @@ struct PrefillShape {
   static constexpr int kWavesPerSimd = WPE;           // occupancy the register budget targets
   // Bias table in LDS, for the layout where every token of the sequence shares
   // one per-head table (token stride 0): log2(e) * rel[dist] at index
-  // kBiasPad + dist, zeros for dist outside [0, rel_extent).  A wave's tile
+  // kBiasTop - dist (descending, so that a lane's 16 keys, whose distances
+  // fall, read ascending addresses), zeros for dist outside [0, rel_extent),
+  // dist from -kBiasPad to kBiasLdsMax + kBiasPad - 1.  A wave's tile
   // that has bias sees dist (over all 32 * NQB lanes' rows, valid or not, and
   // the BK keys) in an interval of 32 * NQB + BK - 1 values that meets
   // [0, rel_extent), so a padding of 32 * NQB + BK - 2 on both sides covers
@@ -255,7 +257,7 @@ __device__ __forceinline__ int tile_chunks(const PrefillParams& p, const TileRan
   return min(max(n, 1), p.n_chunks);
 }
 
-template <typename Sh, int D, typename Tag, typename Rel, bool kProj>
+template <typename Sh, int D, typename Tag, typename Rel, bool kProj, bool kTab>
 __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
     Sh::kWavesPerSimd, Sh::kWavesPerSimd))) void prefill_fwd_kernel(PrefillParams p) {
   using E = Elem<Tag>;
@@ -263,6 +265,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   constexpr int kNqb = Sh::kNqb, kBlockQ = Sh::kBlockQ;
   constexpr int kBlockK = Sh::kBlockK, kThreads = Sh::kThreads, kBiasPad = Sh::kBiasPad;
   constexpr int kBiasLdsFloats = 2 * kBiasPad + kBiasLdsMax;
+  constexpr int kBiasTop = kBiasLdsMax + kBiasPad - 1;  // table index of dist 0
   constexpr int kDBlocks = D / 32;
   constexpr int kKSteps = D / 16;
 
@@ -271,7 +274,8 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   // per fragment instead of one per fragment and stage).
   __shared__ __align__(1024) uint16_t stages[2 * St::kElems];
   // bias table (shared-table layout); with kProj, one projection tile per wave
-  __shared__ __align__(16) float bias_lds[kProj ? 4 : kBiasLdsFloats];
+  constexpr bool kTable = kTab && !kProj;  // the shared bias table, staged in LDS
+  __shared__ __align__(16) float bias_lds[kTable ? kBiasLdsFloats : 4];
   __shared__ __align__(16) float mproj[kProj ? Sh::kWaves * 32 * kProjPitch : 4];
   static_assert(!kProj || (kNqb == 1 && kBlockK == 64), "projection tiles: 32 rows x 64 keys");
   uint16_t* const stage0 = stages;
@@ -376,6 +380,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
       qf[qb][kk] = buf_load_16(rq, (uint32_t)(qi[qb] * p.q_st + 16 * kk + 8 * half) * 2);
 
   const float c2 = p.scale_log2;  // softmax_scale * log2(e)
+  const float inv_c2 = 1.f / c2;   // bias (log2 units) -> score units
   float m_run[kNqb];               // running max (log2 domain), same in both halves
   float l_run[kNqb];               // partial row sum over this half's keys
   f32x16_t o[kNqb][kDBlocks];
@@ -451,9 +456,10 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
       static_cast<const char*>(p.rel) + ((int64_t)qs * p.rel_st + (int64_t)head * p.rel_sh) *
                                             Rel::kBytes,
       span_bytes(lq, p.rel_st, kProj ? kProjDim : p.rel_width, Rel::kBytes));
-  // Shared-table layout with a table short enough to stage in LDS.
-  const bool bias_in_lds =
-      !kProj && IFA4_BIAS_LDS && p.rel_st == 0 && rext > 0 && rext <= kBiasLdsMax;
+  // Shared-table layout with a table short enough to stage in LDS (the host
+  // launches the kTab instantiation for it: token stride 0, rel_extent <=
+  // kBiasLdsMax); the other instantiation reads per-token rows.
+  const bool bias_in_lds = kTable && rext > 0;
   // Fused projection.  W^T [rel_width, 16] fp32 (64-byte rows) stays in L2;
   // rows outside [0, rel_extent) read as zero, so the projected bias is zero
   // there with no further test.  The B operand (this lane's row of r, channels
@@ -600,7 +606,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
     uint32_t w[Rel::kBytes == 4 ? 16 : 9];
     bool slow;  // wave-uniform: one load per element
   };
-  constexpr bool kTokEarly = IFA4_BIAS_EARLY && !kProj && Rel::kBytes == 2;
+  constexpr bool kTokEarly = IFA4_BIAS_EARLY && !kProj && !kTable && Rel::kBytes == 2;
   auto tok_issue = [&](int rel_row, int dtop, bool valid, TokRaw& t) {
     constexpr int kSpan = Rel::kBytes == 2 ? 18 : 16;
     const int lo = rel_row + dtop - 15;
@@ -775,9 +781,103 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
     // ---- logits (log2 domain) and tile max ---------------------------------------
     // Element (blk, e) of a lane is tile-local key 32*blk + 16*half + e; `kc`
     // below drops the lane term, which is folded into the bounds.
-    float sc;  // factor applied inside the exponent FMA
+    // log2(e) * bias of this lane's 16 keys in key block blk (element e at
+    // dist = dbase - 32 blk - e); only on tiles that meet the band
+    auto tile_bias = [&](int qb, int blk, float* bias) {
+      const int dbase = qi[qb] + delta - kb - 16 * half;  // dist = dbase - kc
+      if constexpr (kTable) {
+        // element e at dist = dbase - kc: a constant offset from one base
+        int j0 = kBiasTop - dbase;  // table index of the lane's key 0
+        asm("" : "+v"(j0));          // one base address, the keys as read offsets
+        const float* tb = bias_lds + j0;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) bias[e] = tb[32 * blk + e];
+      } else if constexpr (kProj) {
+        proj_bias(kb, blk, bias);
+      } else {
+        const int rel_row = qi[qb] * (int)p.rel_st;  // element offset of the row
+        if constexpr (kTokEarly)
+          tok_finish(rel_row, dbase - 32 * blk, row_ok[qb], traw[qb][blk], bias);
+        else
+          token_bias(rel_row, dbase - 32 * blk, row_ok[qb], bias);
+      }
+    };
+    // key-range mask as an additive -inf: visible iff lo <= 16 half + kc <= hi,
+    // one unsigned compare per element (an empty range maps to a start no key
+    // reaches)
+    auto mask_bias = [&](int qb, int blk, float* bias) {
+      int hi = lk - 1 - kb;
+      if (p.causal) hi = min(hi, qi[qb] + qpos - kb);
+      if (!row_ok[qb]) hi = -1;
+      const int lo = wl >= 0 ? qi[qb] + qpos - wl - kb : -1;
+      const bool none = hi < lo;
+      const uint32_t lo_h = none ? 0x80000000u : (uint32_t)(lo - 16 * half);
+      const uint32_t span = none ? 0u : (uint32_t)(hi - lo);
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        bias[e] = (uint32_t)(32 * blk + e) - lo_h <= span ? bias[e] : -INFINITY;
+    };
+    float sc = c2;  // factor applied inside the exponent FMA
     float mx[kNqb];
-    if (need_mask || has_bias) {
+    if constexpr (!kProj) {
+      // Scores stay in score units on every tile (the exponent FMA applies
+      // softmax_scale * log2(e) to all of them).  Tiles in the bias band and
+      // masked tiles (diagonal, window edge, KV tail) add bias / c2 in place,
+      // one FMA per element, with -inf as the bias of a masked key (finite
+      // scores then give -inf); interior tiles keep the products as written.
+      if constexpr (kTable) {
+        // shared table: read on every masked tile too (off the band, the
+        // index is clamped into the table's zero padding)
+        if (need_mask || has_bias) {
+#pragma unroll
+          for (int qb = 0; qb < kNqb; ++qb) {
+            const int dbase = qi[qb] + delta - kb - 16 * half;  // dist = dbase - kc
+            int j0 = min(max(kBiasTop - dbase, 0), kBiasLdsFloats - kBlockK);
+            asm("" : "+v"(j0));  // one base address, the keys as read offsets
+            const float* tb = bias_lds + j0;
+#pragma unroll
+            for (int blk = 0; blk < kBlockK / 32; ++blk) {
+              float bias[16];
+#pragma unroll
+              for (int e = 0; e < 16; ++e) bias[e] = tb[32 * blk + e];
+              if (need_mask) mask_bias(qb, blk, bias);
+#pragma unroll
+              for (int e = 0; e < 16; ++e)
+                s[qb][blk][e] = fmaf(bias[e], inv_c2, s[qb][blk][e]);
+            }
+          }
+        }
+      } else if (need_mask || has_bias) {
+#pragma unroll
+        for (int qb = 0; qb < kNqb; ++qb) {
+#pragma unroll
+          for (int blk = 0; blk < kBlockK / 32; ++blk) {
+            float bias[16];
+            if (has_bias) {
+              tile_bias(qb, blk, bias);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 16; ++e) bias[e] = 0.f;
+            }
+            if (need_mask) mask_bias(qb, blk, bias);
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              s[qb][blk][e] = fmaf(bias[e], inv_c2, s[qb][blk][e]);
+          }
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < kNqb; ++qb) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int blk = 0; blk < kBlockK / 32; ++blk)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) m = fmaxf(m, s[qb][blk][e]);
+        mx[qb] = m * c2;
+      }
+    } else if (need_mask || has_bias) {
+      // fused projection: logits in log2 units on bias and masked tiles (the
+      // per-element form keeps fewer registers live beside the projection)
       sc = 1.f;
 #pragma unroll
       for (int qb = 0; qb < kNqb; ++qb) {
@@ -786,25 +886,11 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
         if (!row_ok[qb]) hi = -1;
         const int lo = wl >= 0 ? qi[qb] + qpos - wl - kb : -1;
         const int hi_h = hi - 16 * half, lo_h = lo - 16 * half;
-        const int dbase = qi[qb] + delta - kb - 16 * half;  // dist = dbase - kc
-        const int rel_row = qi[qb] * (int)p.rel_st;        // element offset of the row
         float m = -INFINITY;
 #pragma unroll
         for (int blk = 0; blk < kBlockK / 32; ++blk) {
           float bias[16];  // log2(e) * bias
-          if (has_bias && bias_in_lds) {
-            // element e at dist = dbase - kc: a constant offset from one base
-            const float* tb = bias_lds + kBiasPad + dbase - (kBlockK - 1);
-#pragma unroll
-            for (int e = 0; e < 16; ++e) bias[e] = tb[kBlockK - 1 - (32 * blk + e)];
-          } else if (has_bias && kProj) {
-            proj_bias(kb, blk, bias);
-          } else if (has_bias) {
-            if constexpr (kTokEarly)
-              tok_finish(rel_row, dbase - 32 * blk, row_ok[qb], traw[qb][blk], bias);
-            else
-              token_bias(rel_row, dbase - 32 * blk, row_ok[qb], bias);
-          }
+          if (has_bias) tile_bias(qb, blk, bias);
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int kc = 32 * blk + e;
@@ -818,7 +904,6 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
         mx[qb] = m;
       }
     } else {
-      sc = c2;
 #pragma unroll
       for (int qb = 0; qb < kNqb; ++qb) {
         float m = -INFINITY;
@@ -1029,8 +1114,8 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   if (bias_in_lds) {
 #pragma unroll
     for (int i = 0; i < kBiasPer; ++i) {
-      const int idx = tid + i * kThreads;  // table index + kBiasPad
-      const int dist = idx - kBiasPad;
+      const int idx = tid + i * kThreads;  // table index
+      const int dist = kBiasTop - idx;
       const uint32_t off = (uint32_t)dist < (uint32_t)rext ? (uint32_t)dist * Rel::kBytes
                                                             : kOutOfRange;
       tab[i] = Rel::load(rrel, off) * kLog2e;
@@ -1210,7 +1295,7 @@ __global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(PrefillPar
   }
 }
 
-template <typename Sh, int D, typename Tag, typename Rel, bool kProj>
+template <typename Sh, int D, typename Tag, typename Rel, bool kProj, bool kTab = false>
 hipError_t launch_prefill_t(const PrefillParams& p_in, hipStream_t stream) {
   PrefillParams p = p_in;
   if (p.n_chunks < 1) p.n_chunks = 1;
@@ -1219,7 +1304,7 @@ hipError_t launch_prefill_t(const PrefillParams& p_in, hipStream_t stream) {
   const int pairs = p.batch * (p.n_heads / p.group);
   p.xcd_pairs = pairs % 8 == 0 ? pairs / 8 : 0;
   if (blocks <= 0) return hipSuccess;
-  hipLaunchKernelGGL((prefill_fwd_kernel<Sh, D, Tag, Rel, kProj>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((prefill_fwd_kernel<Sh, D, Tag, Rel, kProj, kTab>), dim3((unsigned)blocks),
                      dim3(Sh::kThreads), 0, stream, p);
   if constexpr (!kProj) {  // the fused projection never splits
     if (p.chunk_tiles > 0) {
@@ -1238,6 +1323,17 @@ hipError_t launch_prefill_rel(const PrefillParams& p, hipStream_t stream) {
   if (p.wt != nullptr) {  // fused projection: r in bf16 or fp32
     return p.rel_dtype == 2 ? launch_prefill_t<ProjShape, D, Tag, RelF32, true>(p, stream)
                             : launch_prefill_t<ProjShape, D, Tag, RelBf16, true>(p, stream);
+  }
+  // one per-head table shared by every token (token stride 0), short enough
+  // for LDS: the table instantiation; per-token rows (or no bias): the other
+  const bool tab =
+      IFA4_BIAS_LDS && p.rel_st == 0 && p.rel_extent > 0 && p.rel_extent <= kBiasLdsMax;
+  if (tab) {
+    switch (p.rel_dtype) {
+      case 0: return launch_prefill_t<Shape, D, Tag, RelBf16, false, true>(p, stream);
+      case 1: return launch_prefill_t<Shape, D, Tag, RelF16, false, true>(p, stream);
+      default: return launch_prefill_t<Shape, D, Tag, RelF32, false, true>(p, stream);
+    }
   }
   switch (p.rel_dtype) {
     case 0: return launch_prefill_t<Shape, D, Tag, RelBf16, false>(p, stream);
