@@ -262,6 +262,17 @@ struct RelBf16 {
   static __device__ __forceinline__ float load(rsrc_t r, uint32_t off) {
     return __uint_as_float(buf_load_2(r, off) << 16);
   }
+  // x rounded to this type, as the low half of a packed pair (high half 0)
+  static __device__ __forceinline__ uint32_t pack_lo(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  static __device__ __forceinline__ float unpack_lo(uint32_t w) { return __uint_as_float(w << 16); }
+  // acc + lo(w) * lo(sel) + hi(w) * hi(sel): one v_dot2_f32_bf16
+  static __device__ __forceinline__ float dot2(uint32_t w, uint32_t sel, float acc) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w),
+                                           __builtin_bit_cast(bf16x2_t, sel), acc, false);
+  }
   // element 0 / 1 of a packed pair
   static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
   static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -270,6 +281,18 @@ struct RelF16 {
   static constexpr int kBytes = 2;
   static __device__ __forceinline__ float load(rsrc_t r, uint32_t off) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)buf_load_2(r, off));
+  }
+  static __device__ __forceinline__ uint32_t pack_lo(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  static __device__ __forceinline__ float unpack_lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  // acc + lo(w) * lo(sel) + hi(w) * hi(sel): one v_dot2_f32_f16
+  static __device__ __forceinline__ float dot2(uint32_t w, uint32_t sel, float acc) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), __builtin_bit_cast(f16x2_t, sel),
+                                  acc, false);
   }
   static __device__ __forceinline__ float lo(uint32_t w) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));

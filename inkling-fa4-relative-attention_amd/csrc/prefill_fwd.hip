@@ -39,7 +39,8 @@
 // 32-bit.
 //
 // Softmax.  exp2 with softmax_scale*log2(e) folded into one FMA; the bias is
-// pre-multiplied by log2(e).  The running max is only raised when it grows by
+// added in score units (bias / softmax_scale), so every tile shares one
+// exponent form.  The running max is only raised when it grows by
 // more than 2^8 (deferred rescale), which keeps the result exact and skips the
 // O rescale on most tiles.  Row sums accumulate the fp32 P (summing the
 // rounded 16-bit P instead would cost the LSE up to 2^-9 relative on short rows).
@@ -112,7 +113,7 @@ struct PrefillShape {
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kWavesPerSimd = WPE;           // occupancy the register budget targets
   // Bias table in LDS, for the layout where every token of the sequence shares
-  // one per-head table (token stride 0): log2(e) * rel[dist] at index
+  // one per-head table (token stride 0): rel[dist] at index
   // kBiasTop - dist (descending, so that a lane's 16 keys, whose distances
   // fall, read ascending addresses), zeros for dist outside [0, rel_extent),
   // dist from -kBiasPad to kBiasLdsMax + kBiasPad - 1.  A wave's tile
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
       qf[qb][kk] = buf_load_16(rq, (uint32_t)(qi[qb] * p.q_st + 16 * kk + 8 * half) * 2);
 
   const float c2 = p.scale_log2;  // softmax_scale * log2(e)
-  const float inv_c2 = 1.f / c2;   // bias (log2 units) -> score units
+  const float inv_scale = kLog2e / c2;  // bias -> score units (1 / softmax_scale)
   float m_run[kNqb];               // running max (log2 domain), same in both halves
   float l_run[kNqb];               // partial row sum over this half's keys
   f32x16_t o[kNqb][kDBlocks];
@@ -517,7 +518,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
       *reinterpret_cast<f32x4_t*>(dst + 8 * i) =
           f32x4_t{acc[4 * i], acc[4 * i + 1], acc[4 * i + 2], acc[4 * i + 3]};
   };
-  // log2(e) * bias of this lane's 16 keys in key block blk: block blk sees
+  // bias of this lane's 16 keys in key block blk: block blk sees
   // distance blocks 1 - blk (slot 0) and 2 - blk (slot 1); element e sits at
   // position col + 31 - 16 * half - e of the lane's row.  Block 1 serves both
   // key blocks and is projected twice: one accumulator live at a time.
@@ -533,7 +534,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
     if (!(kProjEarly && blk == 0)) proj_fill(kb, blk);
     const float* src = mp + col * (kProjPitch + 1) + 31 - 16 * half;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) bias[e] = src[-e] * kLog2e;
+    for (int e = 0; e < 16; ++e) bias[e] = src[-e];
   };
 
   // Per-token bias of the 16 consecutive keys a lane holds in a 32-key block,
@@ -561,7 +562,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
         const uint32_t off = (uint32_t)dist < (uint32_t)rext
                                  ? (uint32_t)(rel_row + dist) * Rel::kBytes
                                  : kOutOfRange;
-        bias[e] = Rel::load(rrel, off) * kLog2e;
+        bias[e] = Rel::load(rrel, off);
       }
       return;
     }
@@ -587,13 +588,9 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
       }
     }
     const bool in_band = dtop - 15 >= 0 && dtop < rext;
-    if (wave_all(in_band)) {
+    if (!wave_all(in_band)) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) bias[e] *= kLog2e;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        bias[e] = (uint32_t)(dtop - e) < (uint32_t)rext ? bias[e] * kLog2e : 0.f;
+      for (int e = 0; e < 16; ++e) bias[e] = (uint32_t)(dtop - e) < (uint32_t)rext ? bias[e] : 0.f;
     }
   };
   // The same in two halves, so that the vector loads are issued before a tile's
@@ -652,14 +649,41 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
       }
     }
     const bool in_band = dtop - 15 >= 0 && dtop < rext;
-    if (wave_all(in_band)) {
+    if (!wave_all(in_band)) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) bias[e] *= kLog2e;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        bias[e] = (uint32_t)(dtop - e) < (uint32_t)rext ? bias[e] * kLog2e : 0.f;
+      for (int e = 0; e < 16; ++e) bias[e] = (uint32_t)(dtop - e) < (uint32_t)rext ? bias[e] : 0.f;
     }
+  };
+
+  // 16-bit per-token bias with a 1 / softmax_scale that the bias type holds
+  // exactly (any power of two: the reference's 1 / head_dim): each element is
+  // added to its score as one v_dot2 of its (realigned) packed pair with
+  // (1 / softmax_scale, 0) or (0, 1 / softmax_scale), no unpacking.
+  uint32_t dsel_lo = 0, dsel_hi = 0;
+  bool dot_ok = false;
+  if constexpr (kTokEarly) {
+    dsel_lo = Rel::pack_lo(inv_scale);
+    dsel_hi = dsel_lo << 16;
+    dot_ok = Rel::unpack_lo(dsel_lo) == inv_scale;
+  }
+  // s[e] += bias / softmax_scale for the 16 keys of block blk, one dot product
+  // per element, on a block whose 16 distances are all in the band; false (and
+  // nothing added) otherwise
+  auto tok_dot = [&](int rel_row, int dtop, const TokRaw& t, f32x16_t& sv) {
+    const bool in_band = dtop - 15 >= 0 && dtop < rext;
+    if (!dot_ok || t.slow || !wave_all(in_band)) return false;
+    if constexpr (Rel::kBytes == 2) {
+      const int lo = rel_row + dtop - 15;
+      const int start = lo - ((lo + rel_par) & 1);
+      const uint32_t sh = 16u * (uint32_t)(lo - start);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t pr = __builtin_amdgcn_alignbit(t.w[k + 1], t.w[k], sh);
+        sv[15 - 2 * k] = Rel::dot2(pr, dsel_lo, sv[15 - 2 * k]);
+        sv[14 - 2 * k] = Rel::dot2(pr, dsel_hi, sv[14 - 2 * k]);
+      }
+    }
+    return true;
   };
 
   // Lane constants of the LDS fragment reads.
@@ -781,7 +805,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
     // ---- logits (log2 domain) and tile max ---------------------------------------
     // Element (blk, e) of a lane is tile-local key 32*blk + 16*half + e; `kc`
     // below drops the lane term, which is folded into the bounds.
-    // log2(e) * bias of this lane's 16 keys in key block blk (element e at
+    // bias of this lane's 16 keys in key block blk (element e at
     // dist = dbase - 32 blk - e); only on tiles that meet the band
     auto tile_bias = [&](int qb, int blk, float* bias) {
       const int dbase = qi[qb] + delta - kb - 16 * half;  // dist = dbase - kc
@@ -822,9 +846,9 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
     if constexpr (!kProj) {
       // Scores stay in score units on every tile (the exponent FMA applies
       // softmax_scale * log2(e) to all of them).  Tiles in the bias band and
-      // masked tiles (diagonal, window edge, KV tail) add bias / c2 in place,
-      // one FMA per element, with -inf as the bias of a masked key (finite
-      // scores then give -inf); interior tiles keep the products as written.
+      // masked tiles (diagonal, window edge, KV tail) add bias / softmax_scale
+      // in place, one FMA per element, with -inf as the bias of a masked key
+      // (finite scores then give -inf); interior tiles keep the products.
       if constexpr (kTable) {
         // shared table: read on every masked tile too (off the band, the
         // index is clamped into the table's zero padding)
@@ -843,26 +867,50 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
               if (need_mask) mask_bias(qb, blk, bias);
 #pragma unroll
               for (int e = 0; e < 16; ++e)
-                s[qb][blk][e] = fmaf(bias[e], inv_c2, s[qb][blk][e]);
+                s[qb][blk][e] = fmaf(bias[e], inv_scale, s[qb][blk][e]);
             }
           }
         }
-      } else if (need_mask || has_bias) {
+      } else if (has_bias) {
 #pragma unroll
         for (int qb = 0; qb < kNqb; ++qb) {
 #pragma unroll
           for (int blk = 0; blk < kBlockK / 32; ++blk) {
-            float bias[16];
-            if (has_bias) {
-              tile_bias(qb, blk, bias);
-            } else {
-#pragma unroll
-              for (int e = 0; e < 16; ++e) bias[e] = 0.f;
+            bool done = false;
+            if constexpr (kTokEarly) {
+              const int dtop = qi[qb] + delta - kb - 16 * half - 32 * blk;
+              done = tok_dot(qi[qb] * (int)p.rel_st, dtop, traw[qb][blk], s[qb][blk]);
             }
-            if (need_mask) mask_bias(qb, blk, bias);
+            if (done) {
+              if (need_mask) {
+                float keep[16];
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-              s[qb][blk][e] = fmaf(bias[e], inv_c2, s[qb][blk][e]);
+                for (int e = 0; e < 16; ++e) keep[e] = 0.f;
+                mask_bias(qb, blk, keep);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) s[qb][blk][e] += keep[e];
+              }
+            } else {
+              float bias[16];
+              tile_bias(qb, blk, bias);
+              if (need_mask) mask_bias(qb, blk, bias);
+#pragma unroll
+              for (int e = 0; e < 16; ++e)
+                s[qb][blk][e] = fmaf(bias[e], inv_scale, s[qb][blk][e]);
+            }
+          }
+        }
+      } else if (need_mask) {  // masked tile off the band: the mask alone, in place
+#pragma unroll
+        for (int qb = 0; qb < kNqb; ++qb) {
+#pragma unroll
+          for (int blk = 0; blk < kBlockK / 32; ++blk) {
+            float keep[16];
+#pragma unroll
+            for (int e = 0; e < 16; ++e) keep[e] = 0.f;
+            mask_bias(qb, blk, keep);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) s[qb][blk][e] += keep[e];
           }
         }
       }
@@ -889,13 +937,13 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
         float m = -INFINITY;
 #pragma unroll
         for (int blk = 0; blk < kBlockK / 32; ++blk) {
-          float bias[16];  // log2(e) * bias
+          float bias[16];
           if (has_bias) tile_bias(qb, blk, bias);
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int kc = 32 * blk + e;
             float x = s[qb][blk][e] * c2;
-            if (has_bias) x += bias[e];
+            if (has_bias) x = fmaf(bias[e], kLog2e, x);
             if (need_mask) x = (kc >= lo_h && kc <= hi_h) ? x : -INFINITY;
             s[qb][blk][e] = x;
             m = fmaxf(m, x);
@@ -1118,7 +1166,7 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
       const int dist = kBiasTop - idx;
       const uint32_t off = (uint32_t)dist < (uint32_t)rext ? (uint32_t)dist * Rel::kBytes
                                                             : kOutOfRange;
-      tab[i] = Rel::load(rrel, off) * kLog2e;
+      tab[i] = Rel::load(rrel, off);
     }
   }
   // Fused projection: this lane's row of r (channels 8 * half .. +7) as the B
@@ -1147,38 +1195,44 @@ __global__ __launch_bounds__(Sh::kThreads) __attribute__((amdgpu_waves_per_eu(
   }
 
   // ---- epilogue: normalise, store O and LSE (split KV: this chunk's partial) -----
+  // The lane's row and half are derived again from the lane id (v_mbcnt), so
+  // that no register has to carry them across the KV loop.
+  const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int half_e = lane_e >> 5;
 #pragma unroll
   for (int qb = 0; qb < kNqb; ++qb) {
     const float l_tot = add_xor32(l_run[qb]);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    if (row_ok[qb] && nch > 1) {
+    const int qi_e = qa + 32 * qb + (lane_e & 31);
+    const bool ok_e = qi_e < lq;
+    if (ok_e && nch > 1) {
       // normalised O of the chunk (fp32) and its LSE in log2 units
-      const int64_t prow = ((int64_t)chunk * p.n_heads + head) * p.total_q + qs + qi[qb];
+      const int64_t prow = ((int64_t)chunk * p.n_heads + head) * p.total_q + qs + qi_e;
       float* pbase = p.part_o + prow * D;
 #pragma unroll
       for (int db = 0; db < kDBlocks; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          *reinterpret_cast<f32x4_t*>(pbase + 32 * db + 8 * i + 4 * half) =
+          *reinterpret_cast<f32x4_t*>(pbase + 32 * db + 8 * i + 4 * half_e) =
               f32x4_t{o[qb][db][4 * i] * inv, o[qb][db][4 * i + 1] * inv,
                       o[qb][db][4 * i + 2] * inv, o[qb][db][4 * i + 3] * inv};
-      if (half == 0) p.part_lse[prow] = l_tot > 0.f ? m_run[qb] + __log2f(l_tot) : -INFINITY;
-    } else if (row_ok[qb]) {
-      uint16_t* obase = static_cast<uint16_t*>(p.out) + (int64_t)(qs + qi[qb]) * p.o_st +
+      if (half_e == 0) p.part_lse[prow] = l_tot > 0.f ? m_run[qb] + __log2f(l_tot) : -INFINITY;
+    } else if (ok_e) {
+      uint16_t* obase = static_cast<uint16_t*>(p.out) + (int64_t)(qs + qi_e) * p.o_st +
                         (int64_t)head * p.o_sh;
 #pragma unroll
       for (int db = 0; db < kDBlocks; ++db) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int d = 32 * db + 8 * i + 4 * half;
+          const int d = 32 * db + 8 * i + 4 * half_e;
           const u32x2_t w = {E::pack2(o[qb][db][4 * i] * inv, o[qb][db][4 * i + 1] * inv),
                              E::pack2(o[qb][db][4 * i + 2] * inv, o[qb][db][4 * i + 3] * inv)};
           *reinterpret_cast<u32x2_t*>(obase + d) = w;
         }
       }
-      if (p.lse != nullptr && half == 0) {
+      if (p.lse != nullptr && half_e == 0) {
         const float lse = l_tot > 0.f ? (m_run[qb] + __log2f(l_tot)) * kLn2 : -INFINITY;
-        p.lse[(int64_t)head * p.lse_sh + qs + qi[qb]] = lse;
+        p.lse[(int64_t)head * p.lse_sh + qs + qi_e] = lse;
       }
     }
   }
