@@ -398,35 +398,55 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     // some key of the step lies in the bias band 0 <= dist < rel_extent (the
     // step's distances run from delta - k0 down to delta - k0 - 31)
     const bool bias = p.rel_extent > 0 && delta - k0 >= 0 && delta - k0 - (kStep - 1) < p.rel_extent;
-    // Per-token bias of the step: this lane's keys k0 + 16 blk + 4 g + j of head
-    // n, one dword each (a 16-bit element and its neighbour), issued together
-    // before the K/V wait below so that they land with the K/V rows: one buffer
-    // resource over the sequence's bias row (all heads; its base aligned down
-    // to 4 bytes, `rel_skew` the bytes it moved), masked elements past it
-    // (read as zero).  Per-element loads waited for one at a time cost a
-    // bottom-right decode with bias extent 1024 two thirds more time.
-    uint32_t bw[kStep / 16][4];
+    // Per-token bias of the step.  Lane (n, g) holds keys k0 + 16 blk + 4 g + j
+    // of head n: per blk a run of four keys whose distances dt - j (dt = delta
+    // - k0 - 16 blk - 4 g) are four consecutive elements of the head's bias row,
+    // lowest address at j = 3.  One 16-byte load per run (fp32: exactly the
+    // run; 16-bit: the dword-aligned 16 bytes around it, realigned with
+    // v_alignbit), issued before the K/V wait below so that it lands with the
+    // K/V rows, through one buffer resource over the sequence's bias rows (all
+    // heads; base aligned down to 4 bytes, `rel_skew` the bytes it moved):
+    // addresses outside it read as zero, and no 16-byte window straddles its
+    // ends (such a step loads one dword per element instead).  Elements outside
+    // the band are zeroed after the load (only on the steps at its edges).
+    u32x4_t bw[kStep / 16];
     uint32_t rel_skew = 0;
+    bool run_form = false;
     if (bias) {
       const uint64_t row = reinterpret_cast<uint64_t>(p.rel) +
                            (uint64_t)((int64_t)cu.qs * p.rel_st * rel_esz);
       rel_skew = (uint32_t)(row & 3u);
-      // size rounded up to whole dwords: the last element's dword is read whole
-      // (its other bytes share that aligned dword, so they stay on its page)
       const uint32_t bytes =
-          rel_skew + (uint32_t)(((int64_t)(p.n_heads - 1) * p.rel_sh + p.rel_extent) * rel_esz);
-      const rsrc_t rr =
-          make_rsrc_uniform(reinterpret_cast<const void*>(row - rel_skew), (bytes + 3u) & ~3u);
+          (rel_skew +
+           (uint32_t)(((int64_t)(p.n_heads - 1) * p.rel_sh + p.rel_extent) * rel_esz) + 3u) &
+          ~3u;
+      const rsrc_t rr = make_rsrc_uniform(reinterpret_cast<const void*>(row - rel_skew), bytes);
+      // element offsets stay below 2^30 (validation bounds the heads' span)
+      const int hoff = (cu.kvh * g_act + n) * (int)p.rel_sh;
+      // 16-byte loads on a step whose distances are all >= 3 (so no run starts
+      // before the rows) and whose windows all end inside the resource
+      // (block 0 holds the lane's highest addresses)
+      const int dt0 = delta - k0 - 4 * g;
+      const uint32_t b30 = rel_skew + (uint32_t)(hoff + dt0 - 3) * (uint32_t)rel_esz;
+      const bool straddle = n < g_act && dt0 - 3 < p.rel_extent && (b30 & ~3u) + 16u > bytes;
+      run_form = delta - k0 - (kStep - 1) >= 3 && !wave_any(straddle);
 #pragma unroll
       for (int blk = 0; blk < kStep / 16; ++blk) {
+        const int dt = delta - k0 - 16 * blk - 4 * g;
+        const int e3 = hoff + dt - 3;  // element of j = 3
+        const uint32_t b3 = rel_skew + (uint32_t)e3 * (uint32_t)rel_esz;
+        const bool any = n < g_act && dt >= 0 && dt - 3 < p.rel_extent;
+        if (!run_form) {
+          // the step holding distances 0..2 (a run of head 0 could start before
+          // the rows) or a window past the rows' end: one dword per element
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = k0 + 16 * blk + 4 * g + j;
-          const int dist = delta - key;
-          const bool ok = n < g_act && key < c1 && dist >= 0 && dist < p.rel_extent;
-          const uint32_t off =
-              rel_skew + (uint32_t)(((int64_t)(cu.kvh * g_act + n) * p.rel_sh + dist) * rel_esz);
-          bw[blk][j] = buf_load_4(rr, ok ? (off & ~3u) : kOutOfRange);
+          for (int j = 0; j < 4; ++j) {
+            const bool ok = n < g_act && dt - j >= 0 && dt - j < p.rel_extent;
+            const uint32_t off = rel_skew + (uint32_t)(hoff + dt - j) * (uint32_t)rel_esz;
+            bw[blk][j] = buf_load_4(rr, ok ? (off & ~3u) : kOutOfRange);
+          }
+        } else {
+          bw[blk] = buf_load_16(rr, any ? (b3 & ~3u) : kOutOfRange);
         }
       }
     }
@@ -500,23 +520,47 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     float mx = -INFINITY;
 #pragma unroll
     for (int blk = 0; blk < kStep / 16; ++blk) {
+      // raw bias of the lane's 4 keys of this block (zero off the band)
+      float bv[4] = {0.f, 0.f, 0.f, 0.f};
+      if (bias) {
+        const int dt = delta - k0 - 16 * blk - 4 * g;
+        const int hoff = (cu.kvh * g_act + n) * (int)p.rel_sh;
+        if (!run_form) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // the element's half of its dword (16-bit types): by its byte offset
+            const uint32_t off = rel_skew + (uint32_t)(hoff + dt - j) * (uint32_t)rel_esz;
+            const uint32_t hv = (bw[blk][j] >> (8 * (off & 2u))) & 0xffffu;
+            bv[j] = rel_esz == 4      ? __uint_as_float(bw[blk][j])
+                    : p.rel_dtype == 0 ? __uint_as_float(hv << 16)
+                                       : (float)__builtin_bit_cast(_Float16, (uint16_t)hv);
+          }
+        } else if (rel_esz == 4) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bv[j] = __uint_as_float(bw[blk][3 - j]);
+        } else {
+          // 16-bit: the run starts 0 or 2 bytes into bw[blk][0]
+          const uint32_t sh = 8u * ((rel_skew + 2u * (uint32_t)(hoff + dt - 3)) & 2u);
+          const uint32_t p0 = __builtin_amdgcn_alignbit(bw[blk][1], bw[blk][0], sh);  // j = 3, 2
+          const uint32_t p1 = __builtin_amdgcn_alignbit(bw[blk][2], bw[blk][1], sh);  // j = 1, 0
+          const uint32_t h[4] = {p1 >> 16, p1 & 0xffffu, p0 >> 16, p0 & 0xffffu};  // j = 0..3
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            bv[j] = p.rel_dtype == 0 ? __uint_as_float(h[j] << 16)
+                                     : (float)__builtin_bit_cast(_Float16, (uint16_t)h[j]);
+        }
+        if (!wave_all(n >= g_act || (dt - 3 >= 0 && dt < p.rel_extent))) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            bv[j] = (uint32_t)(dt - j) < (uint32_t)p.rel_extent ? bv[j] : 0.f;
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float x = acc[blk][j] * c2;
         if (tail || bias) {
           const int key = k0 + 16 * blk + 4 * g + j;
-          const int dist = delta - key;  // i = 0
-          if (bias && n < g_act && key < c1 && dist >= 0 && dist < p.rel_extent) {
-            // the element's half of its dword (16-bit types): by its byte offset
-            const uint32_t off =
-                rel_skew + (uint32_t)(((int64_t)(cu.kvh * g_act + n) * p.rel_sh + dist) * rel_esz);
-            const uint32_t w = bw[blk][j];
-            const uint32_t h16 = (w >> (8 * (off & 2u))) & 0xffffu;
-            const float b = p.rel_dtype == 2   ? __uint_as_float(w)
-                            : p.rel_dtype == 0 ? __uint_as_float(h16 << 16)
-                                               : (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
-            x += b * kLog2e;
-          }
+          if (bias) x = fmaf(bv[j], kLog2e, x);
           if (key >= c1 || key < cu.kbeg) x = -INFINITY;
         }
         acc[blk][j] = x;
