@@ -69,6 +69,16 @@ namespace ifa4 {
 namespace {
 
 constexpr int kStep = 32;  // keys per pipeline step of a decode wave
+// Stream-K weights: a step counts kUnits units of work, a step with keys in a
+// bottom-right bias band kBandUnits (its bias loads and adds), and the waves
+// take equal ranges of units, so the waves holding caches' ends (where the
+// band is) get fewer steps.
+#ifndef IFA4_DECODE_BAND_UNITS
+#define IFA4_DECODE_BAND_UNITS 7
+#endif
+constexpr int kUnits = 4;
+constexpr int kBandUnits = IFA4_DECODE_BAND_UNITS;
+static_assert(kBandUnits >= kUnits && kBandUnits <= 2 * kUnits, "band step weight");
 
 // K/V stream loads.  Each cache byte is read once per call, so the loads are
 // marked non-temporal: a streaming-read probe over the 580 MB benchmark cache
@@ -169,11 +179,26 @@ __device__ __forceinline__ int wave_incl_scan(int x, int lane) {
 }
 
 // Per-lane view of 64 consecutive sequences (lane i <-> sequence base + i).
+// Work is counted in units (kUnits per step, kBandUnits per band step); each
+// of a sequence's kv heads is a segment of `units` units.
 struct SeqChunk {
   int base;        // first sequence of the chunk (wave-uniform)
-  int total_incl;  // steps of all sequences up to the end of the chunk (uniform)
+  int total_incl;  // units of all sequences up to the end of the chunk (uniform)
   int steps, excl, qs, ks, kbeg, kend, lk;  // this lane's sequence
 };
+
+// Steps of a segment before its first bias-band step (bottom-right alignment
+// puts the last rel_extent keys in the band; top-left decode has no band).
+__device__ __forceinline__ int band_start(const DecodeParams& p, int kbeg, int kend, int lk,
+                                          int steps) {
+  if (!p.bottom_right || p.rel_extent <= 0 || steps <= 0) return steps;
+  const int band0 = max(kbeg, lk - p.rel_extent);  // first key with bias
+  return band0 < kend ? min(steps, (band0 - (kbeg & ~(kStep - 1))) / kStep) : steps;
+}
+// Units of a segment of `steps` steps, nb of them before the band.
+__device__ __forceinline__ int seg_units(int steps, int nb) {
+  return kUnits * nb + kBandUnits * (steps - nb);
+}
 
 // Keys of sequence `seq` in a paged cache: seqused_k clamped to what the
 // table row can address.
@@ -206,21 +231,34 @@ __device__ __forceinline__ SeqChunk load_chunk(const DecodeParams& p, int base, 
     c.kend = kr.kend;
     c.steps = seq_steps(lq, kr);
   }
-  const int incl = wave_incl_scan(c.steps, lane);
-  c.excl = excl0 + incl - c.steps;
+  const int units = seg_units(c.steps, band_start(p, c.kbeg, c.kend, c.lk, c.steps));
+  const int incl = wave_incl_scan(units, lane);
+  c.excl = excl0 + incl - units;
   c.total_incl = excl0 + __builtin_amdgcn_readlane(incl, 63);
   return c;
 }
 
-// Where a global step lives: wave-uniform description of its segment.
+// Where a step lives: wave-uniform description of it and its segment.
 struct Cursor {
   int seq, kvh, step, steps;  // step within the segment, steps of the segment
+  int nb, units;              // steps before the band, units of the segment
   int seg;                    // seq * kv_heads + kvh
-  int seg_g0;                 // global index of the segment's first step
+  int seg_u0;                 // global unit of the segment's first step
   int qs, ks, kbeg, kend, lk;  // keys [kbeg, kend) visible; steps from kbeg & ~31
   int slot;                   // Q slot of the segment (0 / 1)
   bool first;                 // first step of the segment in this wave
 };
+
+// Unit (from the segment's start) where step s of the cursor's segment starts.
+__device__ __forceinline__ int step_unit(const Cursor& cu, int s) {
+  return s < cu.nb ? kUnits * s : kUnits * cu.nb + kBandUnits * (s - cu.nb);
+}
+// First step of the segment that starts at unit u or later (steps if none).
+__device__ __forceinline__ int unit_step(const Cursor& cu, int u) {
+  const int ub = kUnits * cu.nb;
+  const int s = u <= ub ? (u + kUnits - 1) / kUnits : cu.nb + (u - ub + kBandUnits - 1) / kBandUnits;
+  return min(s, cu.steps);
+}
 
 // First key of the cursor's step (a multiple of 32).
 __device__ __forceinline__ int step_key0(const Cursor& cu) {
@@ -251,7 +289,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   const int hkv = p.kv_heads;
   const int g_act = p.group;
 
-  // ---- total steps T (every wave derives the same), this wave's range ----------
+  // ---- total units T (every wave derives the same), this wave's range ----------
+  // A wave computes the steps that start inside its range of units.
   SeqChunk ch = load_chunk<kPaged>(p, 0, 0, lane);
   int total = ch.total_incl;
   for (int b = 64; b < p.batch; b += 64) total = load_chunk<kPaged>(p, b, total, lane).total_incl;
@@ -263,24 +302,33 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   if (g0 >= g1) return;
   if (p.batch > 64) ch = load_chunk<kPaged>(p, 0, 0, lane);
 
-  // Cursor of global step gs (gs only moves forward; the chunk follows it).
-  // Returns steps == 0 if gs lies past the last sequence (cannot happen for
-  // gs < T; the bound keeps the search finite whatever cu_seqlens holds).
-  auto locate = [&](int gs) -> Cursor {
+  // Cursor of the first step that starts at global unit gu or later (gu only
+  // moves forward; the chunk follows it).  Returns steps == 0 if there is none
+  // (gu past the last step start; the bound keeps the search finite whatever
+  // cu_seqlens holds).
+  auto locate = [&](int gu) -> Cursor {
     while (true) {
-      const bool hit = ch.steps > 0 && hkv * (ch.excl + ch.steps) > gs;
+      const int nb_l = band_start(p, ch.kbeg, ch.kend, ch.lk, ch.steps);
+      const int units_l = seg_units(ch.steps, nb_l);
+      const bool hit = units_l > 0 && hkv * (ch.excl + units_l) > gu;
       const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
       if (m != 0) {
         const int L = __builtin_ctzll(m);
         Cursor cu;
         cu.seq = ch.base + L;
         cu.steps = __builtin_amdgcn_readlane(ch.steps, L);
+        cu.nb = __builtin_amdgcn_readlane(nb_l, L);
+        cu.units = __builtin_amdgcn_readlane(units_l, L);
         const int excl = __builtin_amdgcn_readlane(ch.excl, L);
-        const int local = gs - hkv * excl;
-        cu.kvh = local / cu.steps;
-        cu.step = local - cu.kvh * cu.steps;
+        const int local = gu - hkv * excl;
+        cu.kvh = local / cu.units;
         cu.seg = cu.seq * hkv + cu.kvh;
-        cu.seg_g0 = hkv * excl + cu.kvh * cu.steps;
+        cu.seg_u0 = hkv * excl + cu.kvh * cu.units;
+        cu.step = unit_step(cu, local - cu.kvh * cu.units);
+        if (cu.step == cu.steps) {  // no step of this segment starts at gu or later
+          gu = cu.seg_u0 + cu.units;
+          continue;
+        }
         cu.qs = __builtin_amdgcn_readlane(ch.qs, L);
         cu.ks = __builtin_amdgcn_readlane(ch.ks, L);
         cu.kbeg = __builtin_amdgcn_readlane(ch.kbeg, L);
@@ -390,6 +438,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   u32x4_t qf[S::kKSteps];
 
   const int rel_esz = p.rel_dtype == 2 ? 4 : 2;  // bytes per bias element
+  // (o * inv, lse2) of head n -> workspace slot; the lane's head and d offset
+  // are derived again from the lane id (v_mbcnt), so that no register carries
+  // the slot addresses across the stream loop
+  auto put_partial = [&](int slot, float inv, float lse2) {
+    int ln = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(ln));  // computed here, not hoisted out of the loop
+    const int hn = ln & 15, hg = ln >> 4;
+    if (hn < g_act) {
+      float* dst = p.ws_o + ((int64_t)slot * g_act + hn) * D + 4 * hg;
+#pragma unroll
+      for (int db = 0; db < S::kDBlocks; ++db)
+        *reinterpret_cast<f32x4_t*>(dst + 16 * db) = o[db] * inv;
+      if (hg == 0) p.ws_lse[(int64_t)slot * g_act + hn] = lse2;
+    }
+  };
   auto step = [&](const u32x4_t* kr, const u32x4_t* vr, const Cursor& cu, bool last) {
     const int k0 = step_key0(cu);
     const int c1 = cu.kend;
@@ -458,7 +521,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
       if (cu.step == 0 && lane == 0) {
         // this wave holds the segment's first step: record the covering waves
         p.ws_meta[2 * cu.seg] = w;
-        p.ws_meta[2 * cu.seg + 1] = (cu.seg_g0 + cu.steps - 1) / P;
+        p.ws_meta[2 * cu.seg + 1] = (cu.seg_u0 + step_unit(cu, cu.steps - 1)) / P;
       }
     }
     // K rows -> LDS (row-major, padded rows: conflict-free A-operand reads of
@@ -622,18 +685,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     if (!last) return;
     // ---- partial of (segment, wave): normalise, store ------------------------------
     const float l_tot = add_xor32(add_xor16(l_run));  // per head n, all g
-    const int slot = cu.seg + w;
-    if (n < g_act) {
-      const float inv = l_tot > 0.f ? p.v_scale / l_tot : 0.f;  // V scale (1 for 16-bit V)
-      float* dst = p.ws_o + ((int64_t)slot * g_act + n) * D + 4 * g;
-#pragma unroll
-      for (int db = 0; db < S::kDBlocks; ++db)
-        *reinterpret_cast<f32x4_t*>(dst + 16 * db) = o[db] * inv;
-    }
-    if (g == 0 && n < g_act) {
-      const float lse2 = l_tot > 0.f ? m_run + __log2f(l_tot) : -INFINITY;
-      p.ws_lse[(int64_t)slot * g_act + n] = lse2;
-    }
+    const float inv = l_tot > 0.f ? p.v_scale / l_tot : 0.f;  // V scale (1 for 16-bit V)
+    const float lse2 = l_tot > 0.f ? m_run + __log2f(l_tot) : -INFINITY;
+    put_partial(cu.seg + w, inv, lse2);
   };
 
   // ---- stream: loads of the next kNbuf - 1 steps in flight while a step is computed --
@@ -645,25 +699,41 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   u32x4_t kbuf[kNbuf][S::kLoads], vbuf[kNbuf][S::kLoads];
   cur[0] = locate(g0);
   if (cur[0].steps == 0) return;
+  if (cur[0].seg_u0 + step_unit(cur[0], cur[0].step) >= g1) {
+    // No step starts in this wave's range.  If the range lies inside the
+    // segment (between two of its steps' starts), the segment's partials run
+    // over this wave's slot too: an empty one (nothing seen) goes there.
+    if (g0 >= cur[0].seg_u0) {
+#pragma unroll
+      for (int db = 0; db < S::kDBlocks; ++db) o[db] = f32x4_t{};
+      put_partial(cur[0].seg + w, 0.f, -INFINITY);
+    }
+    return;
+  }
   cur[0].first = true;
   load_q(cur[0]);
   load(kbuf[0], vbuf[0], cur[0]);
   live[0] = true;
   // Next cursor after `cu`, with its Q slot (a new segment takes the next slot,
   // whose earlier segment's Q was read into registers kNbuf - 1 steps before).
-  auto next = [&](const Cursor& cu, int gs) -> Cursor {
-    Cursor nx = locate(gs);
-    const bool fresh = nx.seg != cu.seg;
-    nx.slot = fresh ? (cu.slot + 1 == kNbuf ? 0 : cu.slot + 1) : cu.slot;
-    nx.first = fresh;
+  auto next = [&](const Cursor& cu) -> Cursor {
+    if (cu.step + 1 < cu.steps) {
+      Cursor nx = cu;
+      nx.step = cu.step + 1;
+      nx.first = false;
+      return nx;
+    }
+    Cursor nx = locate(cu.seg_u0 + cu.units);
+    nx.slot = cu.slot + 1 == kNbuf ? 0 : cu.slot + 1;
+    nx.first = true;
     return nx;
   };
-  // issue the loads of step g into buffer j, after the step in buffer jp
-  auto issue = [&](int j, int jp, int g) {
-    live[j] = live[jp] && g < g1;
+  // issue the loads of the step after the one in buffer jp into buffer j
+  auto issue = [&](int j, int jp) {
+    live[j] = live[jp];
     if (live[j]) {
-      cur[j] = next(cur[jp], g);
-      live[j] = cur[j].steps > 0;
+      cur[j] = next(cur[jp]);
+      live[j] = cur[j].steps > 0 && cur[j].seg_u0 + step_unit(cur[j], cur[j].step) < g1;
     }
     if (live[j]) {
       if (cur[j].first) load_q(cur[j]);
@@ -671,20 +741,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     }
   };
 #pragma unroll
-  for (int j = 1; j < kNbuf - 1; ++j) issue(j, j - 1, g0 + j);
-  int gs = g0;
+  for (int j = 1; j < kNbuf - 1; ++j) issue(j, j - 1);
   bool more = true;
   while (more) {
 #pragma unroll
     for (int j = 0; j < kNbuf; ++j) {
       if (more) {
-        const int jn = (j + kNbuf - 1) % kNbuf;  // buffer of step gs + kNbuf - 1
+        const int jn = (j + kNbuf - 1) % kNbuf;  // buffer of the step kNbuf - 1 ahead
         const int jp = (j + kNbuf - 2) % kNbuf;  // buffer of the step before it
-        issue(jn, jp, gs + kNbuf - 1);
-        const int j1 = (j + 1) % kNbuf;          // buffer of step gs + 1
+        issue(jn, jp);
+        const int j1 = (j + 1) % kNbuf;          // buffer of the next step
         step(kbuf[j], vbuf[j], cur[j], !live[j1] || cur[j1].first);
         more = live[j1];
-        ++gs;
       }
     }
   }

@@ -12,7 +12,8 @@ Two steps, so that variants are built where hipcc is and timed where the GPU is:
   python -m inkling_fa4.sweep run --dir DIR --workload prefill [--seq 4096] [--steps 30]
         (workloads: prefill = shared bias table; prefill_reference = the reference's own
         benchmark config (batch 1, 4 heads, per-token bf16 bias of extent 1024, split
-        KV); prefill_token = per-token fp32 bias of
+        KV); decode_br1024 = the decode batch bottom-right with a per-token bf16 bias
+        of extent 1024; prefill_token = per-token fp32 bias of
         extent 128; prefill_token1024 = per-token bf16 bias of extent 1024; rproj128 /
         rproj512 / rproj1024 = fused projection of that extent; decode, decode_fp8,
         decode_paged)
@@ -55,6 +56,8 @@ Knobs (macros of the kernel sources):
                    IFA4_DECODE_MAX_PARTS      most waves per (sequence, kv head) cache
                    IFA4_DECODE_WAVES_FP8      the same for an fp8 KV cache (workload decode_fp8)
                    IFA4_DECODE_WAVES_PAGED    the same for a paged cache (workload decode_paged)
+  decode_fwd.hip   IFA4_DECODE_BAND_UNITS     stream-K weight of a bias-band step (4 units = a
+                                              plain step; workload decode_br1024)
                    IFA4_PREFILL_SPLIT_MAX_GRID  largest prefill grid the table splits (split KV)
                    IFA4_PREFILL_CHUNK_PCT     split KV: chunk length, percent of the balanced share
                    IFA4_PREFILL_MIN_CHUNK     split KV: shortest chunk in KV tiles
@@ -172,6 +175,15 @@ def _case(workload, seq, batch=1, heads=4):
                                   torch.bfloat16, seed=21, causal=False),
                 testing.make_case("decode_small", [1] * batch, lens, 8, 2, 128,
                                   torch.bfloat16, seed=22, causal=False))
+    if workload == "decode_br1024":
+        # the decode batch in the serving convention: bottom-right, causal, a
+        # per-token bf16 bias of extent 1024 (the last 1024 keys of every cache)
+        g, lens = testing.decode_lengths()
+        mk = lambda name, lq, lk, seed, gen=None: testing.make_case(  # noqa: E731
+            name, lq, lk, 8, 2, 128, torch.bfloat16, seed=seed, causal=True, rel_extent=1024,
+            rel_table=False, rel_dtype=torch.bfloat16, gen=gen)
+        return (mk("sweep_check", [1] * 3, [300, 5000, 1500], 21),
+                mk("decode_br", [1] * len(lens), lens, 5, g))
     return testing.decode(batch=8, seed=21, causal=False), testing.decode(causal=False)
 
 
@@ -205,6 +217,8 @@ def _call(workload, case, return_lse):
         k8, v8, ks, vs, _ = testing.fp8_kv(case)
         args = (args[0], k8, v8) + args[3:]
         kw = {"k_scale": ks, "v_scale": vs}
+    if workload == "decode_br1024":
+        kw = {"bottom_right": True}
     return lambda: fn(*args, causal=case.causal, window_size=case.window_size,
                       softmax_scale=case.scale, return_lse=return_lse, **kw)
 
@@ -406,7 +420,7 @@ def main(argv=None):
                                               "rproj128", "rproj512", "rproj1024", "decode",
                                               "decode_small", "decode_small_fp8",
                                               "decode_small_paged", "decode_fp8",
-                                              "decode_paged"],
+                                              "decode_paged", "decode_br1024"],
                        default="prefill")
         r.add_argument("--seq", type=int, default=4096)
         r.add_argument("--batch", type=int, default=1,
