@@ -35,6 +35,18 @@
 // w, so the map is one-to-one); the wave holding a segment's first step also
 // records the range of waves that cover the segment.
 //
+// Pair mode (kPair: an fp8 cache, d 128, whose kv heads 2m and 2m + 1 sit side
+// by side in every row).  A segment is (sequence, kv head pair) and a wave
+// loads whole 256-byte rows of both heads, so each step reads two contiguous
+// 8 KiB runs (one kv head per wave would read 128-byte halves of 256-byte
+// rows).  K and V stay fp8 in LDS (both tiles 8 KiB, so two waves per SIMD
+// still fit) and convert to the 16-bit type at the MFMA operand: K rows by
+// 8-byte reads, Vᵀ by transposing 8-bit reads (ds_read_b64_tr_b8).  The query
+// heads of both kv heads share the 16 S^T columns: QK runs each head's
+// half of the row against the same Q registers into two accumulators and a
+// column keeps the one of its own kv head; PV adds each head's Vᵀ times P with
+// the other head's columns zeroed.
+//
 // Pass 2 (decode_combine_kernel): per (head, sequence) merge of the segment's
 // partials by log-sum-exp (16 part groups of a workgroup each merge online,
 // then meet in LDS); writes out (q dtype) and lse (natural log).
@@ -63,6 +75,16 @@
 // the register budget).
 #ifndef IFA4_DECODE_NBUF_FP8
 #define IFA4_DECODE_NBUF_FP8 2
+#endif
+#ifndef IFA4_DECODE_PAIR_OVERLAP
+#define IFA4_DECODE_PAIR_OVERLAP 1
+#endif
+// Pair mode: step buffers per wave and the register budget (waves per SIMD).
+#ifndef IFA4_DECODE_NBUF_PAIR
+#define IFA4_DECODE_NBUF_PAIR 2
+#endif
+#ifndef IFA4_DECODE_WPE_PAIR
+#define IFA4_DECODE_WPE_PAIR 2
 #endif
 
 namespace ifa4 {
@@ -118,6 +140,29 @@ template <int D>
 __device__ __forceinline__ int vswz(int row) {
   constexpr int kRowsPerLine = 128 / D;
   return 2 * ((row / kRowsPerLine) & (D / 16 - 1));
+}
+
+// Pair mode tiles in LDS: fp8 rows of both heads (2 D = 256 bytes) at a pitch
+// of 272 bytes, so that 16 rows read at one column hit 16 distinct bank
+// quads.  The keys of a step are permuted: S^T row 4g + j of key block blk is
+// key 8g + 4 blk + j (pair_key), so a 16-lane group's eight P k-slots are the
+// eight consecutive keys 8g..8g+7.  K holds one key block at a time (16 rows:
+// wave load 2t + blk to tile rows 4t..4t+3), V the whole step.  Vᵀ is read by
+// ds_read_b64_tr_b8: in each 16-lane group, lane 2j (2j + 1) points at bytes
+// 0..7 (8..15) of a 16-byte column block of row j, and lane i receives byte i
+// of the block from rows j = 0..7 (measured on gfx950).
+constexpr int kPairPitch = 272;
+// First key (from the step's first) of S^T rows 4g..4g+3 of key block blk.
+template <bool kPair>
+__device__ __forceinline__ int pair_key(int blk, int g) {
+  return kPair ? 8 * g + 4 * blk : 16 * blk + 4 * g;
+}
+
+// 8 fp8 bytes -> the 16-bit MFMA operand (exact).
+template <typename E>
+__device__ __forceinline__ u32x4_t fp8x8_operand(u32x2_t w) {
+  return u32x4_t{E::template fp8x2<false>(w[0]), E::template fp8x2<true>(w[0]),
+                 E::template fp8x2<false>(w[1]), E::template fp8x2<true>(w[1])};
 }
 
 // 8 fp8 (OCP e4m3) values in two dwords (byte i = element i) -> fp32, exactly;
@@ -265,15 +310,27 @@ __device__ __forceinline__ int step_key0(const Cursor& cu) {
   return (cu.kbeg & ~(kStep - 1)) + cu.step * kStep;
 }
 
-template <int D, typename Tag, int G, bool kPaged, int Eb>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_WPE, 8))) void decode_stream_kernel(DecodeParams p) {
+template <int D, typename Tag, int G, bool kPaged, int Eb, bool kPair>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPair ? IFA4_DECODE_WPE_PAIR : IFA4_DECODE_WPE, 8))) void decode_stream_kernel(DecodeParams p) {
   using E = Elem<Tag>;
   using S = DecodeShape<D, Eb>;
+  static_assert(!kPair || (Eb == 1 && !kPaged && D == 128 && G >= 2 && G <= 8),
+                "pair mode: fp8, d 128");
+  constexpr int kRowE = kPair ? 2 * D : D;  // elements of the K / V row a wave loads
+  using L = DecodeShape<kRowE, Eb>;         // load layout
 
-  __shared__ __align__(16) uint16_t k_lds[kStep * S::kPitch];
-  __shared__ __align__(16) uint16_t v_lds[kStep * D];
+  // 16-bit tiles (K padded rows, V swizzled), or in pair mode the fp8 tiles
+  // (K: 16 rows, V: kStep rows, kPairPitch bytes each)
+  __shared__ __align__(16) uint16_t k_lds[kPair ? 16 * kPairPitch / 2 : kStep * S::kPitch];
+  __shared__ __align__(16) uint16_t v_lds[kPair ? kStep * kPairPitch / 2 : kStep * D];
   using Q = DecodeQ<D, G>;
-  constexpr int kNbuf = Eb == 1 ? IFA4_DECODE_NBUF_FP8 : 2;
+  constexpr int kNbuf = kPair ? IFA4_DECODE_NBUF_PAIR : Eb == 1 ? IFA4_DECODE_NBUF_FP8 : 2;
+  // Loads of the next step in flight while a step computes (pair mode).  The
+  // other formats issue them only while the wave's range lasts; the compiler
+  // then merges the two paths' counts and its wait before a step's LDS writes
+  // also covers the next step's loads, so each wave computes with no loads in
+  // flight -- measured faster for them at their wave counts.
+  constexpr bool kOverlap = kPair && IFA4_DECODE_PAIR_OVERLAP;
   static_assert(kNbuf >= 2 && kNbuf <= 3, "two or three step buffers");
   // One Q slot per step buffer: the segments of the steps in flight hold
   // distinct slots, so a slot is rewritten only after its segment's Q was read.
@@ -282,8 +339,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   const int w = blockIdx.x;
   const int W = p.n_waves;
   const int lane = threadIdx.x;
-  const int r = lane / S::kLpr;  // row layout
-  const int c = lane % S::kLpr;
+  const int r = lane / L::kLpr;  // row layout
+  const int c = lane % L::kLpr;
   const int n = lane & 15;       // S^T layout
   const int g = lane >> 4;
   const int hkv = p.kv_heads;
@@ -370,12 +427,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     }
     const uint32_t k_bytes = (uint32_t)(((int64_t)bmask * p.k_st + D) * Eb);
     const uint32_t v_bytes = (uint32_t)(((int64_t)bmask * p.v_st + D) * Eb);
-    constexpr int kGroups = kStep / S::kGroupRows;
+    constexpr int kGroups = kStep / L::kGroupRows;
     rsrc_t rk[kGroups], rv[kGroups];
 #pragma unroll
     for (int grp = 0; grp < kGroups; ++grp) {
       const int ent = __builtin_amdgcn_readlane(
-          tw, ((k0 + S::kGroupRows * grp) >> p.block_shift) - tw_base);
+          tw, ((k0 + L::kGroupRows * grp) >> p.block_shift) - tw_base);
       const bool ok = (unsigned)ent < (unsigned)p.num_blocks;
       const int64_t eb = ok ? (int64_t)ent : 0;
       rk[grp] = make_rsrc_uniform(k_bytes0 + (eb * p.k_sblk + (int64_t)cu.kvh * p.k_sh) * Eb,
@@ -384,29 +441,31 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
                                   ok ? v_bytes : 0u);
     }
 #pragma unroll
-    for (int i = 0; i < S::kLoads; ++i) {
-      const int key = k0 + S::kRpi * i + r;
+    for (int i = 0; i < L::kLoads; ++i) {
+      const int key = k0 + L::kRpi * i + r;
       const uint32_t row = (uint32_t)(key & bmask);
       const bool valid = key < cu.kend;
-      const int grp = (S::kRpi * i) / S::kGroupRows;
+      const int grp = (L::kRpi * i) / L::kGroupRows;
       kr[i] = kv_load(rk[grp], valid ? row * k_row + 16 * c : kOutOfRange);
       vr[i] = kv_load(rv[grp], valid ? row * v_row + 16 * c : kOutOfRange);
     }
   };
-  auto load = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu) {
+  // on = false (contiguous caches): the same loads through empty resources,
+  // which read zeros and touch no memory
+  auto load = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu, bool on) {
     if constexpr (kPaged) {
       load_paged(kr, vr, cu);
     } else {
       const char* kbase = k_bytes0 + ((int64_t)cu.ks * p.k_st + (int64_t)cu.kvh * p.k_sh) * Eb;
       const char* vbase = v_bytes0 + ((int64_t)cu.ks * p.v_st + (int64_t)cu.kvh * p.v_sh) * Eb;
-      const rsrc_t rk =
-          make_rsrc_uniform(kbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.k_st + D) * Eb));
-      const rsrc_t rv =
-          make_rsrc_uniform(vbase, (uint32_t)(((int64_t)(cu.kend - 1) * p.v_st + D) * Eb));
+      const rsrc_t rk = make_rsrc_uniform(
+          kbase, on ? (uint32_t)(((int64_t)(cu.kend - 1) * p.k_st + kRowE) * Eb) : 0u);
+      const rsrc_t rv = make_rsrc_uniform(
+          vbase, on ? (uint32_t)(((int64_t)(cu.kend - 1) * p.v_st + kRowE) * Eb) : 0u);
       const int k0 = step_key0(cu);
 #pragma unroll
-      for (int i = 0; i < S::kLoads; ++i) {
-        const uint32_t row = (uint32_t)(k0 + S::kRpi * i + r);
+      for (int i = 0; i < L::kLoads; ++i) {
+        const uint32_t row = (uint32_t)(k0 + L::kRpi * i + r);
         kr[i] = kv_load(rk, row * k_row + 16 * c);
         vr[i] = kv_load(rv, row * v_row + 16 * c);
       }
@@ -453,18 +512,24 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
       if (hg == 0) p.ws_lse[(int64_t)slot * g_act + hn] = lse2;
     }
   };
-  auto step = [&](const u32x4_t* kr, const u32x4_t* vr, const Cursor& cu, bool last) {
+  struct StepBias {
+    u32x4_t bw[kStep / 16];
+    uint32_t rel_skew;
+    bool bias, run_form;
+  };
+  // The bias loads of a step (see below); issued before the step's K/V wait.
+  auto bias_loads = [&](const Cursor& cu) -> StepBias {
+    StepBias sb;
     const int k0 = step_key0(cu);
-    const int c1 = cu.kend;
     const int delta = p.bottom_right ? cu.lk - 1 : 1 - cu.lk;  // dist = delta - key (i = 0)
-    const bool tail = k0 + kStep > c1 || k0 < cu.kbeg;
     // some key of the step lies in the bias band 0 <= dist < rel_extent (the
     // step's distances run from delta - k0 down to delta - k0 - 31)
     const bool bias = p.rel_extent > 0 && delta - k0 >= 0 && delta - k0 - (kStep - 1) < p.rel_extent;
-    // Per-token bias of the step.  Lane (n, g) holds keys k0 + 16 blk + 4 g + j
-    // of head n: per blk a run of four keys whose distances dt - j (dt = delta
-    // - k0 - 16 blk - 4 g) are four consecutive elements of the head's bias row,
-    // lowest address at j = 3.  One 16-byte load per run (fp32: exactly the
+    sb.bias = bias;
+    // Per-token bias of the step.  Lane (n, g) holds keys k0 + pair_key(blk, g)
+    // + j of head n: per blk a run of four keys whose distances dt - j (dt =
+    // delta - k0 - pair_key(blk, g)) are four consecutive elements of the
+    // head's bias row, lowest address at j = 3.  One 16-byte load per run (fp32: exactly the
     // run; 16-bit: the dword-aligned 16 bytes around it, realigned with
     // v_alignbit), issued before the K/V wait below so that it lands with the
     // K/V rows, through one buffer resource over the sequence's bias rows (all
@@ -472,7 +537,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     // addresses outside it read as zero, and no 16-byte window straddles its
     // ends (such a step loads one dword per element instead).  Elements outside
     // the band are zeroed after the load (only on the steps at its edges).
-    u32x4_t bw[kStep / 16];
+    u32x4_t* bw = sb.bw;
     uint32_t rel_skew = 0;
     bool run_form = false;
     if (bias) {
@@ -489,13 +554,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
       // 16-byte loads on a step whose distances are all >= 3 (so no run starts
       // before the rows) and whose windows all end inside the resource
       // (block 0 holds the lane's highest addresses)
-      const int dt0 = delta - k0 - 4 * g;
+      const int dt0 = delta - k0 - pair_key<kPair>(0, g);
       const uint32_t b30 = rel_skew + (uint32_t)(hoff + dt0 - 3) * (uint32_t)rel_esz;
       const bool straddle = n < g_act && dt0 - 3 < p.rel_extent && (b30 & ~3u) + 16u > bytes;
       run_form = delta - k0 - (kStep - 1) >= 3 && !wave_any(straddle);
 #pragma unroll
       for (int blk = 0; blk < kStep / 16; ++blk) {
-        const int dt = delta - k0 - 16 * blk - 4 * g;
+        const int dt = delta - k0 - pair_key<kPair>(blk, g);
         const int e3 = hoff + dt - 3;  // element of j = 3
         const uint32_t b3 = rel_skew + (uint32_t)e3 * (uint32_t)rel_esz;
         const bool any = n < g_act && dt >= 0 && dt - 3 < p.rel_extent;
@@ -513,6 +578,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
         }
       }
     }
+    sb.rel_skew = rel_skew;
+    sb.run_form = run_form;
+    return sb;
+  };
+  auto step = [&](const u32x4_t* kr, const u32x4_t* vr, const Cursor& cu, const StepBias& sb,
+                  bool last) {
+    const int k0 = step_key0(cu);
+    const int c1 = cu.kend;
+    const int delta = p.bottom_right ? cu.lk - 1 : 1 - cu.lk;  // dist = delta - key (i = 0)
+    const bool tail = k0 + kStep > c1 || k0 < cu.kbeg;
+    const bool bias = sb.bias;
+    const u32x4_t* bw = sb.bw;
+    const uint32_t rel_skew = sb.rel_skew;
+    const bool run_form = sb.run_form;
     if (cu.first) {
       m_run = -INFINITY;
       l_run = 0.f;
@@ -529,11 +608,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     // fp8 converts to the MFMA type on the way (exact); the K scale is folded
     // into the logit scale, the V scale into the partial's normalisation.
     // Waiting for these loads also completes the (earlier) Q DMA of the segment.
+    // Pair mode stores the fp8 bytes as they are: V rows, and K rows of key
+    // block 0 (block 1 follows once QK has read block 0).
+    auto put_k_pair = [&](int blk) {
 #pragma unroll
-    for (int i = 0; i < S::kLoads; ++i) {
-      const int row = S::kRpi * i + r;
+      for (int t = 0; t < L::kLoads / 2; ++t)
+        *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint8_t*>(k_lds) +
+                                    (4 * t + r) * kPairPitch + 16 * c) = kr[2 * t + blk];
+    };
+    if constexpr (kPair) put_k_pair(0);
+#pragma unroll
+    for (int i = 0; i < L::kLoads; ++i) {
+      const int row = L::kRpi * i + r;
       uint16_t* kdst = k_lds + row * S::kPitch + S::kEpl * c;
-      if constexpr (Eb == 2) {
+      if constexpr (kPair) {
+        *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint8_t*>(v_lds) + row * kPairPitch +
+                                    16 * c) = vr[i];
+      } else if constexpr (Eb == 2) {
         *reinterpret_cast<u32x4_t*>(kdst) = kr[i];
         *reinterpret_cast<u32x4_t*>(v_lds + row * D + 8 * (c ^ vswz<D>(row))) = vr[i];
       } else {
@@ -569,15 +660,44 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
                      : u32x4_t{0, 0, 0, 0};
     }
 
-    // S^T = K Q^T: lane (n, g) gets keys 16*blk + 4*g + j of head n
+    // S^T = K Q^T: lane (n, g) gets keys pair_key(blk, g) + j of head n
     f32x4_t acc[kStep / 16];
+    // pair mode: column n holds a query head of the pair's second kv head
+    const bool hi_head = kPair && n >= (g_act >> 1);
 #pragma unroll
     for (int blk = 0; blk < kStep / 16; ++blk) {
       acc[blk] = f32x4_t{};
-      const uint16_t* krow = k_lds + (16 * blk + n) * S::kPitch + 8 * g;
+      if constexpr (kPair) {
+        if (blk == 1) {  // block 0 has been read: K rows of block 1 replace it
+          wave_lds_sync();
+          put_k_pair(1);
+          wave_lds_sync();
+        }
+        // A = 8 fp8 bytes of tile row n (key pair_key), k-slots 8g..8g+7 of d
+        // block kk of kv head h (byte 128 h + 32 kk + 8 g), converted
+        const uint8_t* krow = reinterpret_cast<const uint8_t*>(k_lds) + n * kPairPitch + 8 * g;
+        f32x4_t acc1{};
 #pragma unroll
-      for (int kk = 0; kk < S::kKSteps; ++kk)
-        acc[blk] = E::mfma16(*reinterpret_cast<const u32x4_t*>(krow + 32 * kk), qf[kk], acc[blk]);
+        for (int kk = 0; kk < S::kKSteps; ++kk) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const u32x4_t a = fp8x8_operand<E>(
+                *reinterpret_cast<const u32x2_t*>(krow + 128 * h + 32 * kk));
+            if (h == 0)
+              acc[blk] = E::mfma16(a, qf[kk], acc[blk]);
+            else
+              acc1 = E::mfma16(a, qf[kk], acc1);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[blk][j] = hi_head ? acc1[j] : acc[blk][j];
+      } else {
+        const uint16_t* krow = k_lds + (16 * blk + n) * S::kPitch + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < S::kKSteps; ++kk)
+          acc[blk] =
+              E::mfma16(*reinterpret_cast<const u32x4_t*>(krow + 32 * kk), qf[kk], acc[blk]);
+      }
     }
 
     float mx = -INFINITY;
@@ -586,7 +706,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
       // raw bias of the lane's 4 keys of this block (zero off the band)
       float bv[4] = {0.f, 0.f, 0.f, 0.f};
       if (bias) {
-        const int dt = delta - k0 - 16 * blk - 4 * g;
+        const int dt = delta - k0 - pair_key<kPair>(blk, g);
         const int hoff = (cu.kvh * g_act + n) * (int)p.rel_sh;
         if (!run_form) {
 #pragma unroll
@@ -622,7 +742,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
       for (int j = 0; j < 4; ++j) {
         float x = acc[blk][j] * c2;
         if (tail || bias) {
-          const int key = k0 + 16 * blk + 4 * g + j;
+          const int key = k0 + pair_key<kPair>(blk, g) + j;
           if (bias) x = fmaf(bv[j], kLog2e, x);
           if (key >= c1 || key < cu.kbeg) x = -INFINITY;
         }
@@ -645,7 +765,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     // P^T as the B operand of O^T += V^T P^T: column n = head, k-slots 0..3 =
-    // keys 4g..4g+3, 4..7 = keys 16+4g..16+4g+3 (where the S^T layout left them)
+    // keys 4g..4g+3, 4..7 = keys 16+4g..16+4g+3 (where the S^T layout left them;
+    // pair mode: keys 8g..8g+7)
     float pv[kStep / 16][4];
 #pragma unroll
     for (int blk = 0; blk < kStep / 16; ++blk) {
@@ -666,8 +787,30 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
     // O^T += V^T P^T on v_mfma_f32_16x16x32: A = V^T (row d, the same key
     // k-slots as P), two transposing reads: 16-lane group g, lane i points at
     // V[k0 + i/4][16 db + 4 (i % 4)] and receives V[k0 .. k0+3][16 db + i].
+    // Pair mode: one 8-bit transposing read per (kv head, d block): lane i
+    // points at bytes 8 (i & 1) .. +7 of the block in key row 8g + i/2 and
+    // receives its d = 16 db + i at keys 8g..8g+7 (the P k-slots); each head's
+    // product sees P with the other head's columns zeroed.
+    if constexpr (kPair) {
+      const u32x4_t pz{0u, 0u, 0u, 0u};
+      const u32x4_t pbh[2] = {hi_head ? pz : pb, hi_head ? pb : pz};
+      const uint8_t* vsrc =
+          reinterpret_cast<const uint8_t*>(v_lds) + (8 * g + (n >> 1)) * kPairPitch + 8 * (n & 1);
 #pragma unroll
-    for (int db = 0; db < S::kDBlocks; ++db) {
+      for (int db = 0; db < S::kDBlocks; ++db) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint8_t* src = vsrc + 128 * h + 16 * db;
+          typedef int i32x2_t __attribute__((ext_vector_type(2)));
+          const u32x2_t w = __builtin_bit_cast(
+              u32x2_t, __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                           (__attribute__((address_space(3))) i32x2_t*)src));
+          o[db] = E::mfma16(fp8x8_operand<E>(w), pbh[h], o[db]);
+        }
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < (kPair ? 0 : S::kDBlocks); ++db) {
       u32x2_t part[2];
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
@@ -696,7 +839,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   // compile-time constants only (the inner loop is unrolled).
   Cursor cur[kNbuf];
   bool live[kNbuf];
-  u32x4_t kbuf[kNbuf][S::kLoads], vbuf[kNbuf][S::kLoads];
+  u32x4_t kbuf[kNbuf][L::kLoads], vbuf[kNbuf][L::kLoads];
   cur[0] = locate(g0);
   if (cur[0].steps == 0) return;
   if (cur[0].seg_u0 + step_unit(cur[0], cur[0].step) >= g1) {
@@ -712,7 +855,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
   }
   cur[0].first = true;
   load_q(cur[0]);
-  load(kbuf[0], vbuf[0], cur[0]);
+  load(kbuf[0], vbuf[0], cur[0], true);
   live[0] = true;
   // Next cursor after `cu`, with its Q slot (a new segment takes the next slot,
   // whose earlier segment's Q was read into registers kNbuf - 1 steps before).
@@ -735,9 +878,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
       cur[j] = next(cur[jp]);
       live[j] = cur[j].steps > 0 && cur[j].seg_u0 + step_unit(cur[j], cur[j].step) < g1;
     }
-    if (live[j]) {
+    if constexpr (kOverlap) {
+      // every path issues the step's loads (past the range through empty
+      // resources), so the wait for a step's rows leaves the next step's in flight
+      if (live[j] && cur[j].first) load_q(cur[j]);
+      load(kbuf[j], vbuf[j], cur[j], live[j]);
+    } else if (live[j]) {
       if (cur[j].first) load_q(cur[j]);
-      load(kbuf[j], vbuf[j], cur[j]);
+      load(kbuf[j], vbuf[j], cur[j], true);
     }
   };
 #pragma unroll
@@ -749,9 +897,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IFA4_DECODE_
       if (more) {
         const int jn = (j + kNbuf - 1) % kNbuf;  // buffer of the step kNbuf - 1 ahead
         const int jp = (j + kNbuf - 2) % kNbuf;  // buffer of the step before it
+        StepBias sb;
+        // with loads in flight across steps, the step's bias loads go out
+        // before the next step's K/V loads, so that waiting for them leaves those
+        // in flight (loads complete in order)
+        if constexpr (kOverlap) sb = bias_loads(cur[j]);
         issue(jn, jp);
+        if constexpr (!kOverlap) sb = bias_loads(cur[j]);
         const int j1 = (j + 1) % kNbuf;          // buffer of the next step
-        step(kbuf[j], vbuf[j], cur[j], !live[j1] || cur[j1].first);
+        step(kbuf[j], vbuf[j], cur[j], sb, !live[j1] || cur[j1].first);
         more = live[j1];
       }
     }
@@ -864,16 +1018,30 @@ template <int D, typename Tag, int G>
 hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   if (p.n_waves > 0) {
     const dim3 grid(p.n_waves), block(64);
-    if (p.kv_fp8) {
+    if (p.kv_pair) {
+      // the host pairs kv heads only for contiguous fp8 caches of d 128 whose
+      // pairs hold 2..8 query heads
+      if constexpr (D == 128 && G >= 2 && G <= 8) {
+        if (!p.kv_fp8 || p.block_table != nullptr) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 1, true>), grid, block, 0,
+                           stream, p);
+      } else {
+        return hipErrorInvalidValue;
+      }
+    } else if (p.kv_fp8) {
       if (p.block_table != nullptr)
-        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 1>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 1, false>), grid, block, 0,
+                           stream, p);
       else
-        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 1>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 1, false>), grid, block, 0,
+                           stream, p);
     } else {
       if (p.block_table != nullptr)
-        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 2>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 2, false>), grid, block, 0,
+                           stream, p);
       else
-        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 2>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 2, false>), grid, block, 0,
+                           stream, p);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -203,21 +203,41 @@ bool key0_only(const ifa4_args* a) {
   return a->causal != 0 && (a->flags & IFA4_FLAG_BOTTOM_RIGHT) == 0;
 }
 
+// The kv heads and group the decode kernels see: the call's own, or pairs of
+// adjacent kv heads of an fp8 cache (ifa4::decode_pairs).
+struct DecodeView {
+  int64_t kv_heads, group;
+  bool pair;
+};
+DecodeView decode_view(const ifa4_args* a, bool fp8, bool paged) {
+  DecodeView v{a->kv_heads, a->n_heads / a->kv_heads, false};
+  if (ifa4::decode_pairs(fp8, paged, a->head_dim, v.kv_heads, v.group, a->k_stride_h,
+                         a->v_stride_h)) {
+    v.kv_heads /= 2;
+    v.group *= 2;
+    v.pair = true;
+  }
+  return v;
+}
+
 int32_t decode_waves(const ifa4_args* a, bool fp8 = false, bool paged = false) {
-  return ifa4::decode_waves_for(a->batch, a->kv_heads, a->max_seqlen_k, key0_only(a), fp8,
-                                paged);
+  const DecodeView v = decode_view(a, fp8, paged);
+  return ifa4::decode_waves_for(a->batch, v.kv_heads, a->max_seqlen_k, key0_only(a), fp8, paged,
+                                v.pair);
 }
 
 // Decode workspace: partial (o, lse) slots, one per (segment, wave) pair that
-// can exist (batch * kv_heads + waves), then the per-segment wave ranges.
+// can exist (batch * kv_heads + waves, in the kernels' view of the kv heads),
+// then the per-segment wave ranges.
 struct DecodeLayout {
   int64_t slots, o_bytes, lse_bytes, meta_bytes;
   int64_t total() const { return o_bytes + lse_bytes + meta_bytes; }
 };
 DecodeLayout decode_layout(const ifa4_args* a, bool fp8 = false, bool paged = false) {
   DecodeLayout l;
-  const int64_t segs = (int64_t)a->batch * a->kv_heads;
-  const int64_t group = a->n_heads / a->kv_heads;
+  const DecodeView v = decode_view(a, fp8, paged);
+  const int64_t segs = (int64_t)a->batch * v.kv_heads;
+  const int64_t group = v.group;
   l.slots = segs + decode_waves(a, fp8, paged);
   l.o_bytes = (l.slots * group * a->head_dim * 4 + 255) / 256 * 256;
   l.lse_bytes = (l.slots * group * 4 + 255) / 256 * 256;
@@ -274,10 +294,11 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
                                          lay.lse_bytes);
   p.q_st = args->q_stride_t;
   p.q_sh = args->q_stride_h;
+  const DecodeView view = decode_view(args, qt != nullptr, kv != nullptr);
   p.k_st = args->k_stride_t;
-  p.k_sh = args->k_stride_h;
+  p.k_sh = args->k_stride_h * (view.pair ? 2 : 1);
   p.v_st = args->v_stride_t;
-  p.v_sh = args->v_stride_h;
+  p.v_sh = args->v_stride_h * (view.pair ? 2 : 1);
   p.rel_st = args->rel_stride_t;
   p.rel_sh = args->rel_stride_h;
   p.o_st = args->out_stride_t;
@@ -287,8 +308,9 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
   p.total_k = clamp_rows(args->total_k);
   p.batch = args->batch;
   p.n_heads = args->n_heads;
-  p.kv_heads = args->kv_heads;
-  p.group = args->n_heads / args->kv_heads;
+  p.kv_heads = (int32_t)view.kv_heads;
+  p.group = (int32_t)view.group;
+  p.kv_pair = view.pair ? 1 : 0;
   p.rel_extent = args->rel_extent;
   p.causal = args->causal;
   p.bottom_right = (args->flags & IFA4_FLAG_BOTTOM_RIGHT) ? 1 : 0;

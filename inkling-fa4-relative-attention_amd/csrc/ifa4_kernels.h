@@ -76,6 +76,9 @@ struct DecodeParams {
   int32_t rel_dtype;
   int32_t n_waves;   // persistent waves of pass 1 (0: nothing to stream)
   int32_t kv_fp8;    // 1: K and V are fp8 (OCP e4m3), K scale folded into scale_log2
+  // 1: each kv head of these params is a pair of adjacent fp8 kv heads (k_sh,
+  // v_sh = 2 * head_dim, group = both heads' query heads), streamed as whole rows
+  int32_t kv_pair;
   float scale_log2;
   float v_scale;     // multiplies the output (1 for 16-bit V)
   // Paged KV cache (block_table != nullptr): k/v are block pools, key j of

@@ -51,13 +51,20 @@ Knobs (macros of the kernel sources):
   decode_fwd.hip   IFA4_DECODE_WPE            waves per SIMD the stream pass's registers target
                    IFA4_COMBINE_SPLIT         combine of many-part segments over 2 or 4
                                               workgroups per (head, sequence) (0/1)
+                   IFA4_DECODE_BAND_UNITS     stream-K weight of a bias-band step (4 units = a
+                                              plain step; workload decode_br1024)
+                   IFA4_DECODE_PAIR_OVERLAP   fp8 kv head pairs: next step's loads in flight
+                                              while a step computes (0/1)
+                   IFA4_DECODE_NBUF_PAIR      fp8 kv head pairs: step buffers per wave (2/3)
+                   IFA4_DECODE_WPE_PAIR       fp8 kv head pairs: waves per SIMD of the budget
   tile_table.h     IFA4_DECODE_WAVES          persistent waves of the decode stream pass
                    IFA4_DECODE_MIN_STEPS      fewest 32-key steps per wave (small calls)
                    IFA4_DECODE_MAX_PARTS      most waves per (sequence, kv head) cache
                    IFA4_DECODE_WAVES_FP8      the same for an fp8 KV cache (workload decode_fp8)
                    IFA4_DECODE_WAVES_PAGED    the same for a paged cache (workload decode_paged)
-  decode_fwd.hip   IFA4_DECODE_BAND_UNITS     stream-K weight of a bias-band step (4 units = a
-                                              plain step; workload decode_br1024)
+                   IFA4_DECODE_FP8_PAIRS      fp8 caches of d 128 with adjacent kv heads stream
+                                              kv head pairs (0/1; workload decode_fp8)
+                   IFA4_DECODE_WAVES_FP8_PAIR waves of such a pair stream
                    IFA4_PREFILL_SPLIT_MAX_GRID  largest prefill grid the table splits (split KV)
                    IFA4_PREFILL_CHUNK_PCT     split KV: chunk length, percent of the balanced share
                    IFA4_PREFILL_MIN_CHUNK     split KV: shortest chunk in KV tiles

@@ -379,9 +379,14 @@ def test_quant_validation(kw, qkw, paged, expect):
     st = lib.ifa4_decode_quant_fwd(ctypes.byref(a), kv_ref, ctypes.byref(qt), None, 0, None)
     assert st == (_abi.IFA4_EWORKSPACE if expect == _abi.IFA4_OK else expect)
     if expect == _abi.IFA4_OK and not paged:
-        # fp8 streams min(2048, steps) waves: same layout, more partial slots
-        segs, group = 64 * 2, 8 // 2
-        assert ws >= (segs + 2048) * group * (128 + 1) * 4 + segs * 2 * 4
+        if a.kv_heads % 2 == 0 and a.k_stride_h == a.head_dim == 128:
+            # adjacent kv heads of an fp8 cache stream in pairs over min(1024,
+            # steps) waves: a segment is (sequence, kv head pair) of 2 * group heads
+            segs, group, waves = 64 * a.kv_heads // 2, 2 * a.n_heads // a.kv_heads, 1024
+        else:
+            # one kv head per segment over min(2048, steps) waves
+            segs, group, waves = 64 * a.kv_heads, a.n_heads // a.kv_heads, 2048
+        assert ws >= (segs + waves) * group * (128 + 1) * 4 + segs * 2 * 4
         assert ws > lib.ifa4_decode_workspace_bytes(ctypes.byref(a))
     assert lib.ifa4_decode_quant_fwd(ctypes.byref(a), kv_ref, None, 256, 1 << 30, None) == \
         _abi.IFA4_EINVAL

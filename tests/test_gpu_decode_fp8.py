@@ -3,7 +3,7 @@
 The oracle runs on the dequantised keys and values (k8 * k_scale, v8 *
 v_scale in fp32, exactly what the kernel converts), so the bar is the usual
 one: out within atol / rtol 2e-2, lse within 1e-3.  Paged fp8 must equal
-contiguous fp8 bit for bit.
+contiguous fp8 streamed one kv head per wave (the same partition) bit for bit.
 """
 import pytest
 import torch
@@ -59,10 +59,15 @@ def test_fp8_gqa_head_dims_dtypes(cuda, hq, hkv, head_dim, dtype):
     _check(got, _oracle(deq))
 
 
-def test_fp8_bottom_right_bias_and_window(cuda):
-    lens = [5, 130, 700, 2000]
-    case = testing.make_case("fp8_br", [1] * len(lens), lens, 8, 2, 128, torch.bfloat16, seed=31,
-                             causal=True, window_left=300, rel_table=False, rel_std=1.0)
+@pytest.mark.parametrize("hq,hkv,rel_dtype", [(8, 2, torch.float32), (8, 2, torch.bfloat16),
+                                              (4, 4, torch.float16), (6, 2, torch.bfloat16)])
+def test_fp8_bottom_right_bias_and_window(cuda, hq, hkv, rel_dtype):
+    """Bottom-right fp8 decode with a per-token bias and a left window (kv head
+    pairs: the bias gather follows the pair mode's key order)."""
+    lens = [5, 130, 700, 2000, 1025]
+    case = testing.make_case("fp8_br", [1] * len(lens), lens, hq, hkv, 128, torch.bfloat16,
+                             seed=31, causal=True, window_left=300, rel_table=False,
+                             rel_std=1.0, rel_dtype=rel_dtype)
     got, deq = _fp8_decode(case, cuda, bottom_right=True)
     _check(got, _oracle(deq, bottom_right=True))
 
@@ -82,7 +87,8 @@ def test_fp8_paged_equals_contiguous(cuda, block_size, head_dim):
         v_scale=vs)
     torch.cuda.synchronize()
     got = (out.cpu(), lse.cpu())
-    contiguous, _ = _fp8_decode(case, cuda)
+    # a padded head stride keeps the contiguous cache at one kv head per wave
+    contiguous, _ = _fp8_decode_views(case, cuda, 16)
     assert torch.equal(got[0], contiguous[0]) and torch.equal(got[1], contiguous[1])
     _check(got, _oracle(deq))
 
@@ -118,3 +124,69 @@ def test_fp8_one_sequence_split_combine(cuda, keys):
     print(f"fp8 one sequence of {keys} keys", flush=True)
     got, deq = _fp8_decode(case, cuda)
     _check(got, _oracle(deq))
+
+
+def _fp8_decode_views(case, dev, pad):
+    """fp8 decode with K and V passed as views whose head stride is D + pad
+    (pad 0: the contiguous cache, whose adjacent kv heads stream in pairs
+    when the kv heads are even, D is 128 and a pair holds at most 8 query
+    heads; pad 16: every kv head alone)."""
+    k8, v8, ks, vs, deq = testing.fp8_kv(case)
+    t, hkv, d = k8.shape
+
+    def widen(x):
+        if pad == 0:
+            return x.to(dev)
+        w = torch.zeros(t, hkv, d + pad, dtype=torch.uint8)
+        w[:, :, :d] = x.view(torch.uint8)
+        return w.view(x.dtype).to(dev)[:, :, :d]
+
+    kk, vv = widen(k8), widen(v8)
+    assert kk.stride(1) == d + pad and vv.stride(1) == d + pad
+    c = case.to(dev)
+    print(f"fp8 decode {case.name}: heads {c.q.shape[1]}/{hkv}, D {d}, head stride {d + pad}",
+          flush=True)
+    out, lse = inkling_fa4_rel_attention_decode(
+        c.q, kk, vv, c.rel, c.cu_q, c.cu_k, c.max_q, c.max_k, c.rel_extent, causal=c.causal,
+        window_size=c.window_size, softmax_scale=c.scale, return_lse=True, k_scale=ks,
+        v_scale=vs)
+    torch.cuda.synchronize()
+    return (out.cpu(), lse.cpu()), deq
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 2), (8, 2), (6, 2), (16, 4), (8, 8), (16, 2)])
+def test_fp8_kv_head_pairs_and_single_heads(cuda, hq, hkv):
+    """Adjacent kv heads of a d-128 fp8 cache stream in pairs (a wave reads
+    whole rows of both heads; the pair's query heads share the 16 S^T
+    columns, each keeping the logits of its own kv head, and PV adds each
+    head's Vᵀ times P with the other head's columns zeroed).  Pairs of 2, 4,
+    6 and 8 query heads; several pairs (Hkv 4, 8); a group of 8 per kv head
+    (16 per pair: streamed one kv head at a time).  The same cache through
+    views with a padded head stride streams one kv head per wave; both
+    against the oracle on the dequantised K/V."""
+    lens = [1, 2, 31, 32, 33, 100, 1000, 3000, 4097]
+    case = testing.make_case("fp8_pairs", [1] * len(lens), lens, hq, hkv, 128, torch.bfloat16,
+                             seed=hq * 5 + hkv, causal=False, rel_table=False, rel_extent=64,
+                             scale=0.1)
+    for pad in (0, 16):
+        got, deq = _fp8_decode_views(case, cuda, pad)
+        _check(got, _oracle(deq))
+
+
+def test_fp8_pairs_many_short_caches(cuda):
+    """150 sequences of 0..99 keys (empty and one-key caches among them) in
+    kv head pairs: waves cross many pair segments, the cursor reloads sequence
+    chunks, and empty caches own no steps."""
+    g = torch.Generator().manual_seed(17)
+    lens = torch.randint(0, 100, (150,), generator=g).tolist()
+    lens[3] = 0
+    lens[70] = 1
+    lens[140] = 32
+    case = testing.make_case("fp8_short", [1] * 150, lens, 8, 2, 128, torch.bfloat16, seed=18,
+                             causal=False)
+    got, deq = _fp8_decode(case, cuda)
+    live = torch.tensor([n > 0 for n in lens])
+    want = _oracle(deq)
+    torch.testing.assert_close(got[0][live].float(), want[0][live].float(), atol=ATOL, rtol=RTOL)
+    torch.testing.assert_close(got[1][:, live], want[1][:, live], atol=LSE_ATOL, rtol=0)
+    assert (got[0][~live].float() == 0).all() and torch.isneginf(got[1][:, ~live]).all()

@@ -10,10 +10,11 @@ cache lies tens of log2 units above the even step before it: a wave whose
 range holds an even step and the next odd step of one cache rescales O.
 
 Before each GPU call the test rebuilds the wave partition on the host for
-the wave counts the tile table uses (896 for a contiguous 16-bit cache,
-2048 for a paged or fp8 one) and asserts that P >= 2 and that some wave's
-range grows one head's max by more than 8 log2 units after its first step of
-a cache.  The results are then compared with the oracle (fp8: on the
+the wave count the tile table uses (896 for a contiguous 16-bit cache, 2048
+for a paged or fp8 one, 1024 for an fp8 cache of d 128 whose adjacent kv
+heads stream in pairs, a pair's two caches then being one segment) and
+asserts that P >= 2 and that some wave's range grows one head's max by more
+than 8 log2 units after its first step of a cache.  The results are then compared with the oracle (fp8: on the
 dequantised K/V): out within atol/rtol 2e-2, lse within 1e-3.  Reference
 semantics: src/inkling_fa4/reference.py:38-39 (softmax over all keys, then PV).
 """
@@ -30,7 +31,19 @@ from oracle import ref_rel_attn_paged_with_lse, ref_rel_attn_with_lse
 ATOL, RTOL, LSE_ATOL = 2e-2, 2e-2, 1e-3
 STEP = 32
 RESCALE_LOG2 = 8.0
-WAVE_COUNTS = (896, 2048)  # contiguous 16-bit; paged or fp8 (the tile table)
+
+
+def _view(fmt, head_dim):
+    """(waves, kv heads streamed in pairs) of a cache format, as the tile table
+    streams the 8 / 2-head cases here."""
+    if fmt == "bf16":
+        return 896, False
+    if fmt == "fp8" and head_dim == 128:
+        return 1024, True
+    return 2048, False
+
+
+FORMATS = ("bf16", "paged", "fp8", "fp8_paged")
 # the table's small-call caps: steps per wave; waves per cache (or one per
 # PART_STEPS steps of a longer cache)
 MIN_STEPS, MAX_PARTS, PART_STEPS = 2, 128, 2
@@ -49,25 +62,29 @@ def _sawtooth(case, period=64, lo=0.05, hi=5.0):
     return replace(case, k=(case.k.float() * f[:, None, None]).to(case.k.dtype))
 
 
-def _step_maxima(case):
-    """Per (sequence, kv head): [steps, group] maxima of the logits (log2 units)
-    of each 32-key step, non-causal top-left decode (every key visible)."""
+def _step_maxima(case, pair=False):
+    """Per segment, (sequence, kv head) or with `pair` (sequence, pair of kv
+    heads): [steps, query heads] maxima of the logits (log2 units) of each
+    32-key step, non-causal top-left decode (every key visible)."""
     cq, ck = case.cu_q.tolist(), case.cu_k.tolist()
     hq, hkv = case.q.shape[1], case.k.shape[1]
     g = hq // hkv
+    per = 2 if pair else 1
     out = []
     for b in range(len(ck) - 1):
         q = case.q[cq[b]].float()  # [Hq, D]
         k = case.k[ck[b]:ck[b + 1]].float()  # [L, Hkv, D]
         n = k.shape[0]
-        for kh in range(hkv):
+        for kp in range(hkv // per):
             if n == 0:
-                out.append(torch.zeros(0, g))
+                out.append(torch.zeros(0, per * g))
                 continue
-            s = (k[:, kh] @ q[kh * g:(kh + 1) * g].T) * case.scale * math.log2(math.e)
+            s = torch.cat([(k[:, kh] @ q[kh * g:(kh + 1) * g].T)
+                           for kh in range(per * kp, per * kp + per)], 1)
+            s = s * case.scale * math.log2(math.e)
             steps = (n + STEP - 1) // STEP
-            pad = torch.full((steps * STEP - n, g), -math.inf)
-            out.append(torch.cat([s, pad]).view(steps, STEP, g).amax(1))
+            pad = torch.full((steps * STEP - n, per * g), -math.inf)
+            out.append(torch.cat([s, pad]).view(steps, STEP, per * g).amax(1))
     return out
 
 
@@ -110,13 +127,14 @@ def _case(head_dim, seed):
     return _sawtooth(case)
 
 
-def _assert_drives_rescale(case):
-    maxima = _step_maxima(case)
-    for w in WAVE_COUNTS:
-        p, hits = _rescale_waves(maxima, w, case.max_k, len(LENS_K), case.k.shape[1])
-        print(f"waves {w}: {p} steps per wave, {hits} waves rescale inside their range",
-              flush=True)
-        assert p >= 2 and hits > 0
+def _assert_drives_rescale(case, fmt, head_dim):
+    w, pair = _view(fmt, head_dim)
+    maxima = _step_maxima(case, pair)
+    segs_per_seq = case.k.shape[1] // (2 if pair else 1)
+    p, hits = _rescale_waves(maxima, w, case.max_k, len(LENS_K), segs_per_seq)
+    print(f"{fmt} d{head_dim}, waves {w}: {p} steps per wave, {hits} waves rescale inside "
+          f"their range", flush=True)
+    assert p >= 2 and hits > 0
 
 
 def _compare(out, lse, want):
@@ -127,19 +145,19 @@ def _compare(out, lse, want):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["bf16", "paged", "fp8", "fp8_paged"])
+@pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("head_dim", [128, 64])
 def test_decode_in_wave_rescale(cuda, fmt, head_dim):
     case = _case(head_dim, seed=40 + head_dim)
     fp8 = fmt.startswith("fp8")
     if fp8:
         k8, v8, ks, vs, deq = testing.fp8_kv(case)
-        _assert_drives_rescale(deq)
+        _assert_drives_rescale(deq, fmt, head_dim)
         want = ref_rel_attn_with_lse(deq.q, deq.k, deq.v, deq.rel, deq.cu_q, deq.cu_k,
                                      deq.scale, deq.rel_extent, causal=False)
         kk, vv, kw = k8, v8, dict(k_scale=ks, v_scale=vs)
     else:
-        _assert_drives_rescale(case)
+        _assert_drives_rescale(case, fmt, head_dim)
         want = None
         kk, vv, kw = case.k, case.v, {}
     c = case.to(cuda)
@@ -171,8 +189,9 @@ def test_decode_in_wave_rescale(cuda, fmt, head_dim):
 def test_sawtooth_case_drives_rescale_on_host(head_dim):
     """CPU side of the GPU test: the case and its fp8 copy drive the rescale."""
     case = _case(head_dim, seed=40 + head_dim)
-    _assert_drives_rescale(case)
-    _assert_drives_rescale(testing.fp8_kv(case)[4])
+    deq = testing.fp8_kv(case)[4]
+    for fmt in FORMATS:
+        _assert_drives_rescale(deq if fmt.startswith("fp8") else case, fmt, head_dim)
 
 
 def test_partition_model_detects_planted_flat_keys():
