@@ -14,7 +14,8 @@ Two steps, so that variants are built where hipcc is and timed where the GPU is:
         benchmark config (batch 1, 4 heads, per-token bf16 bias of extent 1024, split
         KV); decode_br1024 = the decode batch bottom-right with a per-token bf16 bias
         of extent 1024; prefill_token = per-token fp32 bias of
-        extent 128; prefill_token1024 = per-token bf16 bias of extent 1024; rproj128 /
+        extent 128; prefill_token1024 = per-token bf16 bias of extent 1024;
+        prefill_table1024 = one shared bf16 bias row of extent 1024; rproj128 /
         rproj512 / rproj1024 = fused projection of that extent; decode, decode_fp8,
         decode_paged)
         [--counters SQ_VALU_MFMA_BUSY_CYCLES,GRBM_GUI_ACTIVE] [--out table.md]
@@ -174,6 +175,15 @@ def _case(workload, seq, batch=1, heads=4):
             name, lens, lens, 8, 2, 128, torch.bfloat16, seed=seed, rel_extent=ext,
             rel_table=False, rel_dtype=rd)
         return mk("sweep_check", [1300, 64, 33], 2), mk("per_token", [seq] * 8, 3)
+    if workload == "prefill_table1024":
+        # one bf16 bias row of extent 1024 shared by every token (token stride 0):
+        # the shared-table path, or with IFA4_BIAS_LDS=0 the per-token gather
+        # reading a bias that stays in cache -- what the gather costs besides
+        # its HBM bytes
+        mk = lambda name, lens, seed: testing.make_case(  # noqa: E731
+            name, lens, lens, 8, 2, 128, torch.bfloat16, seed=seed, rel_extent=1024,
+            rel_table=True, rel_dtype=torch.bfloat16)
+        return mk("sweep_check", [1300, 64, 33], 2), mk("table1024", [seq] * 8, 3)
     if workload.startswith("decode_small"):
         # --batch sequences of --seq cached keys each (serving at small batch);
         # _fp8 / _paged: the same keys as an fp8 or a paged cache
@@ -423,7 +433,7 @@ def main(argv=None):
     for name in ("run", "measure"):
         r = sub.add_parser(name)
         r.add_argument("--workload", choices=["prefill", "prefill_reference", "prefill_token",
-                                              "prefill_token1024",
+                                              "prefill_token1024", "prefill_table1024",
                                               "rproj128", "rproj512", "rproj1024", "decode",
                                               "decode_small", "decode_small_fp8",
                                               "decode_small_paged", "decode_fp8",
