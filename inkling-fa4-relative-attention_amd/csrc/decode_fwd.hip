@@ -9,10 +9,12 @@
 // causal keeps every key, the window keeps j >= Lk - 1 - window_left.
 //
 // Work decomposition.  A "segment" is one (sequence, kv head); it holds the
-// 32-key steps of its visible keys (decode_keys).  All segments' steps are laid end to end
-// (sequence-major, kv head minor) and W persistent waves (about one resident
-// round on the chip) each take an equal contiguous range of P = ceil(T / W)
-// steps.  A wave therefore streams K/V without gaps across segment
+// 32-key steps of its visible keys (decode_keys).  All segments' steps are laid
+// end to end (sequence-major, kv head minor), weighted in units (kUnits per
+// step, kBandUnits per step with bias), and W persistent waves (about one
+// resident round on the chip) each take an equal contiguous range of P =
+// ceil(T / W) units, computing the steps that start in it.  A wave therefore
+// streams K/V without gaps across segment
 // boundaries; where its range leaves a segment it writes one (o, lse) partial
 // and carries on (no wave ends after each split, which would hold its slot
 // until its stores drain: measured 11.8 us of 117 on the benchmark batch).
