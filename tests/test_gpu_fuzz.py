@@ -128,6 +128,28 @@ def test_decode_fp8_random_configs(cuda, seed):
     _check(deq, out, lse, br)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_decode_fp8_pair_random_configs(cuda, seed):
+    """Random configs held to the fp8 caches whose adjacent kv heads stream in
+    pairs (d 128, an even number of kv heads, at most 4 query heads each)."""
+    lens_q, lens_k, _, _, _, dtype, opts, br = _draw(4500 + seed, decode=True)
+    r = random.Random(seed)
+    hkv = r.choice([2, 4, 6])
+    hq = hkv * r.choice([1, 2, 3, 4])
+    if sum(lens_k) == 0:
+        lens_k[0] = 5
+    case = testing.make_case(f"fuzzp{seed}", lens_q, lens_k, hq, hkv, 128, dtype, seed=seed,
+                             **opts)
+    k8, v8, ks, vs, deq = testing.fp8_kv(case)
+    c = case.to(cuda)
+    out, lse = inkling_fa4_rel_attention_decode(
+        c.q, k8.to(cuda), v8.to(cuda), c.rel, c.cu_q, c.cu_k, c.max_q, c.max_k, c.rel_extent,
+        causal=c.causal, window_size=c.window_size, softmax_scale=c.scale, return_lse=True,
+        bottom_right=br, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    _check(deq, out, lse, br)
+
+
 @pytest.mark.parametrize("seed", range(12))
 def test_rproj_random_configs(cuda, seed):
     lens_q, lens_k, hq, hkv, d, dtype, opts, br = _draw(5000 + seed, decode=False)
