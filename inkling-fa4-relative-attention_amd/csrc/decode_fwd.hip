@@ -37,8 +37,8 @@
 // w, so the map is one-to-one); the wave holding a segment's first step also
 // records the range of waves that cover the segment.
 //
-// Pair mode (kPair: an fp8 cache, d 128, whose kv heads 2m and 2m + 1 sit side
-// by side in every row).  A segment is (sequence, kv head pair) and a wave
+// Pair mode (kPair: an fp8 cache, d 128, contiguous or paged, whose kv heads
+// 2m and 2m + 1 sit side by side in every row).  A segment is (sequence, kv head pair) and a wave
 // loads whole 256-byte rows of both heads, so each step reads two contiguous
 // 8 KiB runs (one kv head per wave would read 128-byte halves of 256-byte
 // rows).  K and V stay fp8 in LDS (both tiles 8 KiB, so two waves per SIMD
@@ -316,8 +316,7 @@ template <int D, typename Tag, int G, bool kPaged, int Eb, bool kPair>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPair ? IFA4_DECODE_WPE_PAIR : IFA4_DECODE_WPE, 8))) void decode_stream_kernel(DecodeParams p) {
   using E = Elem<Tag>;
   using S = DecodeShape<D, Eb>;
-  static_assert(!kPair || (Eb == 1 && !kPaged && D == 128 && G >= 2 && G <= 8),
-                "pair mode: fp8, d 128");
+  static_assert(!kPair || (Eb == 1 && D == 128 && G >= 2 && G <= 8), "pair mode: fp8, d 128");
   constexpr int kRowE = kPair ? 2 * D : D;  // elements of the K / V row a wave loads
   using L = DecodeShape<kRowE, Eb>;         // load layout
 
@@ -417,25 +416,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPair ? IFA4
   // entries outside the pool read as zero.
   int tw = -1, tw_seq = -1, tw_base = 0;
   const int bmask = (1 << p.block_shift) - 1;
-  auto load_paged = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu) {
+  auto load_paged = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu, bool on) {
     const int k0 = step_key0(cu);
     const int blk0 = k0 >> p.block_shift;
-    if (cu.seq != tw_seq || blk0 < tw_base || blk0 >= tw_base + 64) {
+    if (on && (cu.seq != tw_seq || blk0 < tw_base || blk0 >= tw_base + 64)) {
       tw_seq = cu.seq;
       tw_base = blk0 & ~63;
       const int nblk = (cu.lk + bmask) >> p.block_shift;
       const int e = tw_base + lane;
       tw = e < nblk ? p.block_table[(int64_t)cu.seq * p.bt_stride + e] : -1;
     }
-    const uint32_t k_bytes = (uint32_t)(((int64_t)bmask * p.k_st + D) * Eb);
-    const uint32_t v_bytes = (uint32_t)(((int64_t)bmask * p.v_st + D) * Eb);
+    const uint32_t k_bytes = (uint32_t)(((int64_t)bmask * p.k_st + kRowE) * Eb);
+    const uint32_t v_bytes = (uint32_t)(((int64_t)bmask * p.v_st + kRowE) * Eb);
     constexpr int kGroups = kStep / L::kGroupRows;
     rsrc_t rk[kGroups], rv[kGroups];
 #pragma unroll
     for (int grp = 0; grp < kGroups; ++grp) {
       const int ent = __builtin_amdgcn_readlane(
           tw, ((k0 + L::kGroupRows * grp) >> p.block_shift) - tw_base);
-      const bool ok = (unsigned)ent < (unsigned)p.num_blocks;
+      const bool ok = on && (unsigned)ent < (unsigned)p.num_blocks;
       const int64_t eb = ok ? (int64_t)ent : 0;
       rk[grp] = make_rsrc_uniform(k_bytes0 + (eb * p.k_sblk + (int64_t)cu.kvh * p.k_sh) * Eb,
                                   ok ? k_bytes : 0u);
@@ -452,11 +451,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kPair ? IFA4
       vr[i] = kv_load(rv[grp], valid ? row * v_row + 16 * c : kOutOfRange);
     }
   };
-  // on = false (contiguous caches): the same loads through empty resources,
-  // which read zeros and touch no memory
+  // on = false: the same loads through empty resources, which read zeros and
+  // touch no memory
   auto load = [&](u32x4_t* kr, u32x4_t* vr, const Cursor& cu, bool on) {
     if constexpr (kPaged) {
-      load_paged(kr, vr, cu);
+      load_paged(kr, vr, cu, on);
     } else {
       const char* kbase = k_bytes0 + ((int64_t)cu.ks * p.k_st + (int64_t)cu.kvh * p.k_sh) * Eb;
       const char* vbase = v_bytes0 + ((int64_t)cu.ks * p.v_st + (int64_t)cu.kvh * p.v_sh) * Eb;
@@ -1021,12 +1020,16 @@ hipError_t launch_decode_g(const DecodeParams& p, hipStream_t stream) {
   if (p.n_waves > 0) {
     const dim3 grid(p.n_waves), block(64);
     if (p.kv_pair) {
-      // the host pairs kv heads only for contiguous fp8 caches of d 128 whose
-      // pairs hold 2..8 query heads
+      // the host pairs kv heads only for fp8 caches of d 128 whose pairs hold
+      // 2..8 query heads
       if constexpr (D == 128 && G >= 2 && G <= 8) {
-        if (!p.kv_fp8 || p.block_table != nullptr) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 1, true>), grid, block, 0,
-                           stream, p);
+        if (!p.kv_fp8) return hipErrorInvalidValue;
+        if (p.block_table != nullptr)
+          hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, true, 1, true>), grid, block, 0,
+                             stream, p);
+        else
+          hipLaunchKernelGGL((decode_stream_kernel<D, Tag, G, false, 1, true>), grid, block, 0,
+                             stream, p);
       } else {
         return hipErrorInvalidValue;
       }

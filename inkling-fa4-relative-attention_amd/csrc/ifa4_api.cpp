@@ -209,10 +209,9 @@ struct DecodeView {
   int64_t kv_heads, group;
   bool pair;
 };
-DecodeView decode_view(const ifa4_args* a, bool fp8, bool paged) {
+DecodeView decode_view(const ifa4_args* a, bool fp8) {
   DecodeView v{a->kv_heads, a->n_heads / a->kv_heads, false};
-  if (ifa4::decode_pairs(fp8, paged, a->head_dim, v.kv_heads, v.group, a->k_stride_h,
-                         a->v_stride_h)) {
+  if (ifa4::decode_pairs(fp8, a->head_dim, v.kv_heads, v.group, a->k_stride_h, a->v_stride_h)) {
     v.kv_heads /= 2;
     v.group *= 2;
     v.pair = true;
@@ -221,7 +220,7 @@ DecodeView decode_view(const ifa4_args* a, bool fp8, bool paged) {
 }
 
 int32_t decode_waves(const ifa4_args* a, bool fp8 = false, bool paged = false) {
-  const DecodeView v = decode_view(a, fp8, paged);
+  const DecodeView v = decode_view(a, fp8);
   return ifa4::decode_waves_for(a->batch, v.kv_heads, a->max_seqlen_k, key0_only(a), fp8, paged,
                                 v.pair);
 }
@@ -235,7 +234,7 @@ struct DecodeLayout {
 };
 DecodeLayout decode_layout(const ifa4_args* a, bool fp8 = false, bool paged = false) {
   DecodeLayout l;
-  const DecodeView v = decode_view(a, fp8, paged);
+  const DecodeView v = decode_view(a, fp8);
   const int64_t segs = (int64_t)a->batch * v.kv_heads;
   const int64_t group = v.group;
   l.slots = segs + decode_waves(a, fp8, paged);
@@ -294,7 +293,7 @@ int32_t run_decode(const ifa4_args* args, const ifa4_paged_kv* kv, const ifa4_kv
                                          lay.lse_bytes);
   p.q_st = args->q_stride_t;
   p.q_sh = args->q_stride_h;
-  const DecodeView view = decode_view(args, qt != nullptr, kv != nullptr);
+  const DecodeView view = decode_view(args, qt != nullptr);
   p.k_st = args->k_stride_t;
   p.k_sh = args->k_stride_h * (view.pair ? 2 : 1);
   p.v_st = args->v_stride_t;

@@ -94,10 +94,11 @@ constexpr int64_t kDecodeMinSteps = IFA4_DECODE_MIN_STEPS;
 constexpr int64_t kDecodeMaxParts = IFA4_DECODE_MAX_PARTS;
 constexpr int64_t kDecodePartSteps = IFA4_DECODE_PART_STEPS;
 
-// fp8 caches of d 128 whose kv heads sit side by side in every row (head
-// stride = head_dim) stream their kv heads in pairs, one wave over whole rows
-// of both (a pair holds at most 8 query heads); the kernel then sees half the
-// kv heads, twice the group and 32-key steps of twice the bytes.
+// fp8 caches of d 128 (contiguous or paged) whose kv heads sit side by side in
+// every row (head stride = head_dim) stream their kv heads in pairs, one wave
+// over whole rows of both (a pair holds at most 8 query heads); the kernel
+// then sees half the kv heads, twice the group and 32-key steps of twice the
+// bytes.
 #ifndef IFA4_DECODE_FP8_PAIRS
 #define IFA4_DECODE_FP8_PAIRS 1
 #endif
@@ -105,9 +106,16 @@ constexpr int64_t kDecodePartSteps = IFA4_DECODE_PART_STEPS;
 #define IFA4_DECODE_WAVES_FP8_PAIR 1024
 #endif
 constexpr int64_t kDecodeWavesFp8Pair = IFA4_DECODE_WAVES_FP8_PAIR;
-inline bool decode_pairs(bool fp8, bool paged, int64_t head_dim, int64_t kv_heads, int64_t group,
+// (paged: 1536, as for one kv head per wave more waves hide the block-table
+// window refills; batch 64 at blocks of 16, one box: 64.5 us at 1024, 59.6 at
+// 1536, 60.4-60.9 at 2048, against 66.0 streaming one kv head per wave)
+#ifndef IFA4_DECODE_WAVES_FP8_PAIR_PAGED
+#define IFA4_DECODE_WAVES_FP8_PAIR_PAGED 1536
+#endif
+constexpr int64_t kDecodeWavesFp8PairPaged = IFA4_DECODE_WAVES_FP8_PAIR_PAGED;
+inline bool decode_pairs(bool fp8, int64_t head_dim, int64_t kv_heads, int64_t group,
                          int64_t k_stride_h, int64_t v_stride_h) {
-  return IFA4_DECODE_FP8_PAIRS && fp8 && !paged && head_dim == 128 && kv_heads % 2 == 0 &&
+  return IFA4_DECODE_FP8_PAIRS && fp8 && head_dim == 128 && kv_heads % 2 == 0 &&
          2 * group <= 8 && k_stride_h == head_dim && v_stride_h == head_dim;
 }
 
@@ -118,7 +126,7 @@ inline int32_t decode_waves_for(int64_t batch, int64_t kv_heads, int64_t max_seq
   int64_t w = kDecodeWaves;
   if (paged && kDecodeWavesPaged > w) w = kDecodeWavesPaged;
   if (fp8 && kDecodeWavesFp8 > w) w = kDecodeWavesFp8;
-  if (pair) w = kDecodeWavesFp8Pair;
+  if (pair) w = paged ? kDecodeWavesFp8PairPaged : kDecodeWavesFp8Pair;
   const int64_t by_steps = (t + kDecodeMinSteps - 1) / kDecodeMinSteps;
   const int64_t seg_steps = batch * kv_heads > 0 ? t / (batch * kv_heads) : 0;
   const int64_t long_parts = (seg_steps + kDecodePartSteps - 1) / kDecodePartSteps;

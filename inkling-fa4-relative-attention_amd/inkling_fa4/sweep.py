@@ -17,7 +17,7 @@ Two steps, so that variants are built where hipcc is and timed where the GPU is:
         extent 128; prefill_token1024 = per-token bf16 bias of extent 1024;
         prefill_table1024 = one shared bf16 bias row of extent 1024; rproj128 /
         rproj512 / rproj1024 = fused projection of that extent; decode, decode_fp8,
-        decode_paged)
+        decode_paged, decode_paged_fp8)
         [--counters SQ_VALU_MFMA_BUSY_CYCLES,GRBM_GUI_ACTIVE] [--out table.md]
   python -m inkling_fa4.sweep split [--shapes reference,headline] [--seqs 1024,4096]
         (split-KV prefill against the unsplit kernel, in-tree build)
@@ -66,6 +66,8 @@ Knobs (macros of the kernel sources):
                    IFA4_DECODE_FP8_PAIRS      fp8 caches of d 128 with adjacent kv heads stream
                                               kv head pairs (0/1; workload decode_fp8)
                    IFA4_DECODE_WAVES_FP8_PAIR waves of such a pair stream
+                   IFA4_DECODE_WAVES_FP8_PAIR_PAGED  the same for a paged cache (workload
+                                              decode_paged_fp8)
                    IFA4_PREFILL_SPLIT_MAX_GRID  largest prefill grid the table splits (split KV)
                    IFA4_PREFILL_CHUNK_PCT     split KV: chunk length, percent of the balanced share
                    IFA4_PREFILL_MIN_CHUNK     split KV: shortest chunk in KV tiles
@@ -223,13 +225,20 @@ def _call(workload, case, return_lse):
           else inkling_fa4_rel_attention_decode)
     args = case.args()
     kw = {}
-    if workload in ("decode_paged", "decode_small_paged"):  # blocks of 16, shuffled
-        pk = testing.paginate(case.to("cpu"), block_size=16, seed=0, spare_blocks=0,
+    if workload in ("decode_paged", "decode_small_paged", "decode_paged_fp8"):
+        # blocks of 16, shuffled (decode_paged_fp8: an fp8 cache, per-tensor scales)
+        kw = {}
+        src = case.to("cpu")
+        if workload == "decode_paged_fp8":
+            k8, v8, ks, vs, _ = testing.fp8_kv(src)
+            src = testing.replace(src, k=k8, v=v8)
+            kw = {"k_scale": ks, "v_scale": vs}
+        pk = testing.paginate(src, block_size=16, seed=0, spare_blocks=0,
                               fill=0.0).to(case.q.device)
         return lambda: inkling_fa4_rel_attention_decode_paged(
             case.q, pk.k_cache, pk.v_cache, case.rel, case.cu_q, pk.seqused_k, pk.block_table,
             case.max_q, case.max_k, case.rel_extent, causal=case.causal,
-            window_size=case.window_size, softmax_scale=case.scale, return_lse=return_lse)
+            window_size=case.window_size, softmax_scale=case.scale, return_lse=return_lse, **kw)
     if workload in ("decode_fp8", "decode_small_fp8"):  # fp8 cache, per-tensor scales
         k8, v8, ks, vs, _ = testing.fp8_kv(case)
         args = (args[0], k8, v8) + args[3:]
@@ -437,7 +446,8 @@ def main(argv=None):
                                               "rproj128", "rproj512", "rproj1024", "decode",
                                               "decode_small", "decode_small_fp8",
                                               "decode_small_paged", "decode_fp8",
-                                              "decode_paged", "decode_br1024"],
+                                              "decode_paged", "decode_br1024",
+                                              "decode_paged_fp8"],
                        default="prefill")
         r.add_argument("--seq", type=int, default=4096)
         r.add_argument("--batch", type=int, default=1,

@@ -2,8 +2,10 @@
 
 The oracle runs on the dequantised keys and values (k8 * k_scale, v8 *
 v_scale in fp32, exactly what the kernel converts), so the bar is the usual
-one: out within atol / rtol 2e-2, lse within 1e-3.  Paged fp8 must equal
-contiguous fp8 streamed one kv head per wave (the same partition) bit for bit.
+one: out within atol / rtol 2e-2, lse within 1e-3.  Paged fp8 must match
+contiguous fp8 up to the order of the split merge (the same per-step arithmetic,
+kv head pairs at d 128, one kv head per wave at d 64; a paged cache streams with
+more waves): lse within 1e-5, out within one 16-bit rounding step.
 """
 import pytest
 import torch
@@ -39,6 +41,13 @@ def _oracle(deq, bottom_right=False):
 def _check(got, want):
     torch.testing.assert_close(got[0].float(), want[0].float(), atol=ATOL, rtol=RTOL)
     torch.testing.assert_close(got[1], want[1], atol=LSE_ATOL, rtol=0)
+
+
+def _same(a, b):
+    """Paged against contiguous: the same keys and per-step arithmetic, another
+    stream-K split."""
+    torch.testing.assert_close(a[0].float(), b[0].float(), atol=1e-3, rtol=1e-2)
+    torch.testing.assert_close(a[1], b[1], atol=1e-5, rtol=0)
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -87,9 +96,8 @@ def test_fp8_paged_equals_contiguous(cuda, block_size, head_dim):
         v_scale=vs)
     torch.cuda.synchronize()
     got = (out.cpu(), lse.cpu())
-    # a padded head stride keeps the contiguous cache at one kv head per wave
-    contiguous, _ = _fp8_decode_views(case, cuda, 16)
-    assert torch.equal(got[0], contiguous[0]) and torch.equal(got[1], contiguous[1])
+    contiguous, _ = _fp8_decode(case, cuda)
+    _same(got, contiguous)
     _check(got, _oracle(deq))
 
 
@@ -190,3 +198,29 @@ def test_fp8_pairs_many_short_caches(cuda):
     torch.testing.assert_close(got[0][live].float(), want[0][live].float(), atol=ATOL, rtol=RTOL)
     torch.testing.assert_close(got[1][:, live], want[1][:, live], atol=LSE_ATOL, rtol=0)
     assert (got[0][~live].float() == 0).all() and torch.isneginf(got[1][:, ~live]).all()
+
+
+@pytest.mark.parametrize("block_size", [8, 32])
+def test_fp8_paged_pairs_bottom_right_bias(cuda, block_size):
+    """kv head pairs of a paged fp8 cache, bottom-right with a per-token bf16 bias
+    and a left window: the contiguous pair stream's results up to the merge
+    order, and both held to the oracle."""
+    lens = [5, 130, 700, 2000, 1025, 33]
+    case = testing.make_case("fp8_pbr", [1] * len(lens), lens, 8, 2, 128, torch.bfloat16,
+                             seed=34, causal=True, window_left=300, rel_table=False,
+                             rel_std=1.0, rel_dtype=torch.bfloat16, rel_extent=512)
+    k8, v8, ks, vs, deq = testing.fp8_kv(case)
+    pk = testing.paginate(testing.replace(case, k=k8, v=v8), block_size=block_size, seed=5,
+                          fill=0.0)
+    c, p = case.to(cuda), pk.to(cuda)
+    out, lse = inkling_fa4_rel_attention_decode_paged(
+        c.q, p.k_cache, p.v_cache, c.rel, c.cu_q, p.seqused_k, p.block_table, c.max_q, c.max_k,
+        c.rel_extent, causal=True, window_size=c.window_size, softmax_scale=c.scale,
+        return_lse=True, bottom_right=True, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    got = (out.cpu(), lse.cpu())
+    contiguous, _ = _fp8_decode(case, cuda, bottom_right=True)
+    _same(got, contiguous)
+    want = _oracle(deq, bottom_right=True)
+    _check(got, want)
+    _check(contiguous, want)

@@ -11,8 +11,9 @@ range holds an even step and the next odd step of one cache rescales O.
 
 Before each GPU call the test rebuilds the wave partition on the host for
 the wave count the tile table uses (896 for a contiguous 16-bit cache, 2048
-for a paged or fp8 one, 1024 for an fp8 cache of d 128 whose adjacent kv
-heads stream in pairs, a pair's two caches then being one segment) and
+for a paged or fp8 one, 1024 / 1536 for a contiguous / paged fp8 cache of d 128
+whose adjacent kv heads stream in pairs, a pair's two caches then being one
+segment) and
 asserts that P >= 2 and that some wave's range grows one head's max by more
 than 8 log2 units after its first step of a cache.  The results are then compared with the oracle (fp8: on the
 dequantised K/V): out within atol/rtol 2e-2, lse within 1e-3.  Reference
@@ -40,6 +41,8 @@ def _view(fmt, head_dim):
         return 896, False
     if fmt == "fp8" and head_dim == 128:
         return 1024, True
+    if fmt == "fp8_paged" and head_dim == 128:
+        return 1536, True
     return 2048, False
 
 
