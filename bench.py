@@ -302,23 +302,27 @@ def decode_bench(steps, warmup, block_size=0, fp8=False):
     table_bytes = 0
     c = case.to("cuda")
     args = c.args()
+    kw = {}
     if fp8:
         k8, v8, ks, vs, _ = testing.fp8_kv(case)
-        k8, v8 = k8.to("cuda"), v8.to("cuda")
-
-        def step():
-            return inkling_fa4_rel_attention_decode(
-                c.q, k8, v8, c.rel, c.cu_q, c.cu_k, c.max_q, c.max_k, c.rel_extent,
-                causal=False, softmax_scale=c.scale, k_scale=ks, v_scale=vs)
-    elif block_size:
-        pk = testing.paginate(case, block_size=block_size, seed=0, spare_blocks=0,
+        kw = {"k_scale": ks, "v_scale": vs}
+    if block_size:
+        src = testing.replace(case, k=k8, v=v8) if fp8 else case
+        pk = testing.paginate(src, block_size=block_size, seed=0, spare_blocks=0,
                               fill=0.0).to("cuda")
         table_bytes = 4 * int(((lens_k + block_size - 1) // block_size).sum())
 
         def step():
             return inkling_fa4_rel_attention_decode_paged(
                 c.q, pk.k_cache, pk.v_cache, c.rel, c.cu_q, pk.seqused_k, pk.block_table,
-                c.max_q, c.max_k, c.rel_extent, causal=False, softmax_scale=c.scale)
+                c.max_q, c.max_k, c.rel_extent, causal=False, softmax_scale=c.scale, **kw)
+    elif fp8:
+        k8, v8 = k8.to("cuda"), v8.to("cuda")
+
+        def step():
+            return inkling_fa4_rel_attention_decode(
+                c.q, k8, v8, c.rel, c.cu_q, c.cu_k, c.max_q, c.max_k, c.rel_extent,
+                causal=False, softmax_scale=c.scale, **kw)
     else:
         def step():
             return inkling_fa4_rel_attention_decode(*args, causal=False, softmax_scale=c.scale)
@@ -577,6 +581,12 @@ def main():
         log(f"decode fp8: {d8['us']:.1f} us  {d8['gbps']:.0f} GB/s")
         result["decode_fp8"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                 for k, v in d8.items()}
+        if not args.no_sweep:
+            log(f"decode, paged fp8 cache (block 16): {args.steps} steps")
+            dp8 = decode_bench(args.steps, args.warmup, block_size=16, fp8=True)
+            log(f"decode paged fp8: {dp8['us']:.1f} us  {dp8['gbps']:.0f} GB/s")
+            result["decode_paged_fp8"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                          for k, v in dp8.items()}
         if not args.no_sweep:  # (kept out of profiling runs: same kernel, other shapes)
             result["decode_small_batch"] = decode_small_bench(args.steps, args.warmup)
             dbr = decode_bottom_right_bench(args.steps, args.warmup)
