@@ -390,3 +390,41 @@ def test_quant_validation(kw, qkw, paged, expect):
         assert ws > lib.ifa4_decode_workspace_bytes(ctypes.byref(a))
     assert lib.ifa4_decode_quant_fwd(ctypes.byref(a), kv_ref, None, 256, 1 << 30, None) == \
         _abi.IFA4_EINVAL
+
+
+def _fp8_ws(paged=False, **kw):
+    lib = _abi.lib()
+    a = _decode_args(cu_seqlens_k=7 * _P, total_k=600000, **kw)
+    kv = _paged_ok(block_size=16, max_blocks_per_seq=1024) if paged else None
+    qt = _abi.make_quant(k_scale=0.01, v_scale=0.02)
+    return lib.ifa4_decode_quant_workspace_bytes(ctypes.byref(a),
+                                                 ctypes.byref(kv) if kv is not None else None,
+                                                 ctypes.byref(qt))
+
+
+def _layout_bytes(segs, group, waves):
+    """Decode workspace layout: (segments + waves) partial slots of group heads,
+    o rows of 128 fp32 and one lse each (both 256-byte aligned), 2 ints per segment."""
+    slots = segs + waves
+    o = (slots * group * 128 * 4 + 255) // 256 * 256
+    lse = (slots * group * 4 + 255) // 256 * 256
+    return o + lse + segs * 2 * 4
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_fp8_decode_kv_head_pair_layouts(paged):
+    """An fp8 cache of d 128 whose adjacent kv heads sit side by side in each row
+    streams them in pairs: the workspace is laid out for batch x Hkv/2 segments
+    of 2 x group heads over 1024 waves (1536 for a paged cache).  A padded head
+    stride, an odd number of kv heads or more than 8 query heads per pair keep one
+    kv head per segment over 2048 waves."""
+    pair_waves = 1536 if paged else 1024
+    assert _fp8_ws(paged) == _layout_bytes(64 * 1, 8, pair_waves)
+    assert _fp8_ws(paged, n_heads=16, kv_heads=4) == _layout_bytes(64 * 2, 8, pair_waves)
+    assert _fp8_ws(paged, n_heads=6, kv_heads=2) == _layout_bytes(64 * 1, 6, pair_waves)
+    # unpaired: strided heads, 3 kv heads, a group of 8 (16 query heads per pair)
+    assert _fp8_ws(paged, k_stride_h=144, v_stride_h=144, k_stride_t=2 * 144,
+                   v_stride_t=2 * 144) == _layout_bytes(64 * 2, 4, 2048)
+    assert _fp8_ws(paged, n_heads=6, kv_heads=3, k_stride_t=3 * 128,
+                   v_stride_t=3 * 128) == _layout_bytes(64 * 3, 2, 2048)
+    assert _fp8_ws(paged, n_heads=16, kv_heads=2) == _layout_bytes(64 * 2, 8, 2048)
