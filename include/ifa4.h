@@ -206,11 +206,14 @@ int32_t ifa4_prefill_count_tiles(const ifa4_args* args, const int32_t* host_cu_s
  * Decode: exactly one query token per sequence (total_q == batch, and
  * cu_seqlens_q = arange(batch + 1), which only the device reads: the rows of a
  * sequence with another query count get out = 0 and lse = -inf).  Split-KV,
- * stream-K: pass 1 runs min(W, steps) persistent waves (W from the tile table:
- * 896 for 16-bit K/V, 2048 for fp8; ifa4_decode_tile reports it) over all
- * (sequence, kv head) caches laid end to end in 32-key steps, each wave an
- * equal range; it writes one (o, lse) partial per (cache, wave) it touches
- * into the workspace.  Pass 2 merges each cache's partials by log-sum-exp and
+ * stream-K: pass 1 runs up to W persistent waves (W from the tile table: 896
+ * for a contiguous 16-bit cache, 2048 for a paged one; for an fp8 cache 1024
+ * when adjacent kv heads stream in pairs, 1536 paged, else 2048; fewer for
+ * small calls) over all (sequence, kv head) caches laid end to end in 32-key
+ * steps, each wave an equal range of work (a step whose keys carry bias
+ * counts 7/4 of a plain one; ifa4_decode_tile reports the keys per wave of a
+ * contiguous 16-bit cache); it writes one (o, lse) partial per (cache, wave)
+ * it touches into the workspace.  Pass 2 merges each cache's partials by log-sum-exp and
  * writes out/lse.  The workspace (ifa4_decode_workspace_bytes, 256-byte
  * aligned, contents on entry irrelevant) is scratch for one call; calls that
  * share a workspace must not overlap.  Replaces
